@@ -1,0 +1,137 @@
+/*
+ * dflash_hip.h -- C ABI of the MI355X (gfx950) W4A16 qlinear / routed-MoE library.
+ *
+ * Plain C: pointers, sizes and status codes only.  Every entry point is
+ * stream-ordered on the caller's HIP stream (passed as void*), never
+ * allocates or frees device memory, never synchronises, and keeps no pointer
+ * after it returns.  Scratch memory is a caller-provided workspace whose size
+ * comes from the matching *_workspace_bytes() query.  Device pointers must be
+ * 16-byte aligned.
+ *
+ * Weight format (reference model/qwen35_moe_dflash/graph/quant_weights.py:147-148,
+ * graph/quant_plan.py:76-87,165): a logical weight W[E][N][K] is stored as
+ * uint8 [E][N][K/2], signed two's-complement nibbles, k = 2j in the low nibble
+ * of byte j and k = 2j+1 in the high nibble; scales are [E][N][K/G] (bf16 or
+ * fp32), dequantised weight = q * scale[k / G].  Expert banks keep checkpoint
+ * orientation: gate_up [E][2I][H] (gate rows first), down [E][H][I].
+ *
+ * Every function returns DFLASH_OK (0) or a nonzero status; the message of the
+ * last failure on the calling thread is available from dflash_last_error().
+ */
+#ifndef DFLASH_HIP_H
+#define DFLASH_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DFLASH_ABI_VERSION 1
+
+enum dflash_status {
+  DFLASH_OK = 0,
+  DFLASH_ERR_INVALID_ARGUMENT = 1, /* null/misaligned pointer, bad size or layout */
+  DFLASH_ERR_UNSUPPORTED = 2,      /* shape outside what the kernels implement */
+  DFLASH_ERR_WORKSPACE = 3,        /* workspace missing or smaller than queried */
+  DFLASH_ERR_HIP = 4               /* a HIP runtime call or kernel launch failed */
+};
+
+enum dflash_dtype { DFLASH_DTYPE_BF16 = 0, DFLASH_DTYPE_F32 = 1 };
+
+/* One packed int4 matrix (experts == 1) or expert bank (experts == E). */
+typedef struct dflash_w4 {
+  const void* packed;  /* uint8 [experts][rows][cols/2] */
+  const void* scales;  /* [experts][rows][cols/group_size], scale_dtype */
+  int64_t experts;
+  int64_t rows;        /* N: output features */
+  int64_t cols;        /* K: input features */
+  int64_t group_size;  /* 128 or 256 */
+  int32_t scale_dtype; /* enum dflash_dtype */
+} dflash_w4;
+
+/* ABI version of the loaded library (DFLASH_ABI_VERSION). */
+int dflash_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* dflash_last_error(void);
+
+/*
+ * W4A16 quantized linear: y[m][n] = sum_k x[m][k] * q[n][k] * s[n][k/G].
+ * x bf16 [m][K], y bf16 [m][N]; fp32 accumulation, one bf16 rounding.
+ * Replaces the vendor QuantBatchMatmul call of
+ * model/qwen35_moe_dflash/fused/quantization.py:154-165
+ * (OriginalQuantizedWeights.linear; dynamic int8 activation quant is not used:
+ * activations stay bf16 per specs/dflash-contract.json:104-113).
+ * Constraints: N % 32 == 0, K % 512 == 0, group_size in {128, 256}.
+ */
+size_t dflash_qlinear_workspace_bytes(int64_t m, int64_t k, int64_t group_size);
+int dflash_qlinear_w4a16(const void* x, int64_t m, const dflash_w4* weight, void* y, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+/*
+ * Router logits, fp32 [tokens][experts] = hidden bf16 [tokens][H] . router_weight bf16 [E][H]^T,
+ * accumulated in fp32 and not rounded (reference/fused_ops.py:161 computes the
+ * same product; fp32 output keeps routing a function of exact logits).
+ * Constraints: H % 256 == 0.
+ */
+int dflash_router_logits(const void* hidden, int64_t tokens, int64_t hidden_size, const void* router_weight,
+                         int64_t experts, float* logits, void* stream);
+
+/*
+ * Top-k routing + stable expert permutation from fp32 logits [tokens][experts].
+ * Replaces npu_moe_gating_top_k_softmax + renorm + npu_moe_init_routing_v2
+ * (fused/quantization.py:184-192; reference/fused_ops.py:162-164):
+ *   topk_ids     int32 [tokens][k]  experts by descending logit, lowest id on ties
+ *   topk_weights fp32  [tokens][k]  softmax over the selected logits
+ *   perm         int32 [tokens*k]   flat pair t*k+slot at each expert-sorted position
+ *   inv_perm     int32 [tokens*k]   expert-sorted position of each flat pair
+ *   expert_offsets int32 [experts+1] segment starts (tokens_per_expert = diff)
+ * Constraints: experts <= 1024, 0 < k <= min(experts, 64).
+ */
+size_t dflash_moe_route_workspace_bytes(int64_t tokens, int64_t experts, int64_t top_k);
+int dflash_moe_route(const float* logits, int64_t tokens, int64_t experts, int64_t top_k, int32_t* topk_ids,
+                     float* topk_weights, int32_t* perm, int32_t* inv_perm, int32_t* expert_offsets,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Routed-MoE expert FFN over packed banks given a routing (from dflash_moe_route):
+ * per expert segment, h = silu(x.Wg^T) * (x.Wu^T) (bf16), y = h.Wd^T; then
+ * out[t] = sum_slot w[t][slot] * y[t][slot] (+ shared expert) in fp32, one bf16
+ * rounding.  Replaces npu_grouped_matmul x2 + SiLU*up + npu_moe_finalize_routing
+ * (fused/quantization.py:193-199) and the expert loop of reference/fused_ops.py:165-173.
+ * The optional shared expert (shared_gate_up [2I][H], shared_down [H][I],
+ * shared_gate_weight bf16 [H]) adds down(silu(gate(x))*up(x)) * sigmoid(x.w)
+ * (fused/model.py:305-307); pass NULLs to leave it out.
+ * Constraints: H % 512 == 0, I % 512 == 0, experts <= 1024, 0 < k <= 64.
+ */
+size_t dflash_moe_workspace_bytes(int64_t tokens, int64_t hidden_size, int64_t inter_size, int64_t experts,
+                                  int64_t top_k, int64_t group_size, int has_shared);
+int dflash_moe_experts_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, int64_t top_k,
+                             const float* topk_weights, const int32_t* perm, const int32_t* inv_perm,
+                             const int32_t* expert_offsets, const dflash_w4* gate_up, const dflash_w4* down,
+                             const dflash_w4* shared_gate_up, const dflash_w4* shared_down,
+                             const void* shared_gate_weight, void* out, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+/*
+ * Whole routed-MoE layer (+ optional shared expert): router logits (from
+ * router_weight bf16 [E][H], or taken as given when router_logits != NULL),
+ * routing, expert FFN and combine.  The routing outputs are written to the
+ * caller's arrays exactly as dflash_moe_route defines them.  Mirrors
+ * OriginalQuantizedWeights.moe (fused/quantization.py:181-202) and the
+ * FusedOps.moe contract (fused/ops.py:108-123) over packed banks.
+ */
+int dflash_moe_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, const float* router_logits,
+                     const void* router_weight, int64_t top_k, const dflash_w4* gate_up, const dflash_w4* down,
+                     const dflash_w4* shared_gate_up, const dflash_w4* shared_down, const void* shared_gate_weight,
+                     void* out, float* logits_out, int32_t* topk_ids, float* topk_weights, int32_t* perm,
+                     int32_t* inv_perm, int32_t* expert_offsets, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DFLASH_HIP_H */

@@ -1,0 +1,15 @@
+"""MI355X-native (gfx950) W4A16 qlinear and routed-MoE expert FFN.
+
+The directory name is not a Python identifier; load it under the alias
+``qwen35_dflash_amd`` (see ``load_package`` in ``tests/conftest.py`` and
+``bench.py``).  Modules:
+
+* ``fused_ops`` -- FusedOps ABI-v1 adapter module (the drop-in seam)
+* ``ops``       -- PyTorch-ROCm wrappers over the C ABI
+* ``packing``   -- ``PackedW4`` / ``SharedExpert`` types and the int4 packer
+* ``synthetic`` -- seeded synthetic workloads (tests and benchmark)
+* ``_lib``      -- ctypes binding of ``libdflash_hip.so``
+* ``build``     -- hipcc build recipe
+"""
+from . import _lib, fused_ops, ops, packing, synthetic  # noqa: F401
+from .packing import PackedW4, SharedExpert, pack_int4, quantize_w4  # noqa: F401

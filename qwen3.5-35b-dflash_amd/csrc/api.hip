@@ -1,0 +1,399 @@
+// extern "C" entry points of libdflash_hip.so (declared in include/dflash_hip.h).
+//
+// Each entry validates shapes and pointers on the host, carves the caller's
+// workspace, and enqueues kernels on the caller's stream.  No allocation, no
+// synchronisation, no C++ exception crosses the ABI.
+#include <algorithm>
+#include <string>
+
+#include "../../include/dflash_hip.h"
+#include "kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int launch_status(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(DFLASH_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+  return DFLASH_OK;
+}
+
+size_t align256(size_t v) { return (v + 255u) & ~static_cast<size_t>(255u); }
+
+struct Carver {
+  size_t off = 0;
+  size_t take(size_t bytes) {
+    const size_t o = off;
+    off += align256(bytes);
+    return o;
+  }
+};
+
+int check_w4(const dflash_w4* w, const char* name, int64_t experts, int64_t rows, int64_t cols) {
+  if (!w) return fail(DFLASH_ERR_INVALID_ARGUMENT, std::string(name) + ": descriptor is NULL");
+  if (!w->packed || !w->scales) return fail(DFLASH_ERR_INVALID_ARGUMENT, std::string(name) + ": NULL packed or scales");
+  if (!aligned16(w->packed)) return fail(DFLASH_ERR_INVALID_ARGUMENT, std::string(name) + ": packed weights not 16-byte aligned");
+  if (w->scale_dtype != DFLASH_DTYPE_BF16 && w->scale_dtype != DFLASH_DTYPE_F32)
+    return fail(DFLASH_ERR_INVALID_ARGUMENT, std::string(name) + ": scale_dtype must be BF16 or F32");
+  const size_t sal = w->scale_dtype == DFLASH_DTYPE_F32 ? 4u : 2u;
+  if (reinterpret_cast<uintptr_t>(w->scales) % sal)
+    return fail(DFLASH_ERR_INVALID_ARGUMENT, std::string(name) + ": scales misaligned");
+  if (w->experts != experts || w->rows != rows || w->cols != cols)
+    return fail(DFLASH_ERR_INVALID_ARGUMENT,
+                std::string(name) + ": expected [" + std::to_string(experts) + "," + std::to_string(rows) + "," +
+                    std::to_string(cols) + "], got [" + std::to_string(w->experts) + "," + std::to_string(w->rows) +
+                    "," + std::to_string(w->cols) + "]");
+  if (w->group_size != 128 && w->group_size != 256)
+    return fail(DFLASH_ERR_UNSUPPORTED, std::string(name) + ": group_size must be 128 or 256");
+  if (cols % w->group_size) return fail(DFLASH_ERR_INVALID_ARGUMENT, std::string(name) + ": K not a multiple of group_size");
+  return DFLASH_OK;
+}
+
+// ---------------------------------------------------------------- layouts
+struct RouteLayout {
+  size_t meta, hit, counts, bitmap, total;
+};
+
+RouteLayout route_layout(int64_t T, int64_t E) {
+  Carver c;
+  RouteLayout L;
+  L.meta = c.take(16);
+  L.hit = c.take(4 * static_cast<size_t>(E));
+  L.counts = c.take(4 * static_cast<size_t>(E));
+  L.bitmap = c.take(4 * static_cast<size_t>(T) * ((E + 31) / 32));
+  L.total = c.off;
+  return L;
+}
+
+struct MoeLayout {
+  RouteLayout route;
+  size_t logits, x_il, xneg, gate, h, hpart, y, total;
+};
+
+MoeLayout moe_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int64_t G, bool shared) {
+  MoeLayout L;
+  L.route = route_layout(T, E);
+  Carver c;
+  c.off = L.route.total;
+  const size_t rows = static_cast<size_t>(T) * k + (shared ? T : 0);
+  L.logits = c.take(4 * static_cast<size_t>(T) * E);
+  L.x_il = c.take(2 * static_cast<size_t>(T) * H);
+  L.xneg = c.take(4 * static_cast<size_t>(T) * (H / G));
+  L.gate = c.take(4 * static_cast<size_t>(T));
+  L.h = c.take(2 * rows * I);
+  L.hpart = c.take(4 * rows * (I / 16));
+  L.y = c.take(4 * rows * H);
+  L.total = c.off;
+  return L;
+}
+
+template <typename T>
+T* at(void* base, size_t off) {
+  return reinterpret_cast<T*>(static_cast<char*>(base) + off);
+}
+
+int check_route_args(int64_t T, int64_t E, int64_t k) {
+  if (T < 0) return fail(DFLASH_ERR_INVALID_ARGUMENT, "tokens must be >= 0");
+  if (T > (1 << 24)) return fail(DFLASH_ERR_UNSUPPORTED, "tokens above 2^24 are not supported");
+  if (E <= 0 || E > dflash::kMaxExperts) return fail(DFLASH_ERR_UNSUPPORTED, "experts must be in [1, 1024]");
+  if (k <= 0 || k > E || k > dflash::kMaxTopK)
+    return fail(DFLASH_ERR_INVALID_ARGUMENT, "top_k must be in (0, min(experts, 64)]");
+  return DFLASH_OK;
+}
+
+struct MoeShapes {
+  int64_t T, H, I, E, k, G;
+  bool shared;
+  bool gu_f32, dn_f32;
+};
+
+int check_moe(const void* hidden, int64_t T, int64_t H, int64_t k, const dflash_w4* gate_up, const dflash_w4* down,
+              const dflash_w4* sgu, const dflash_w4* sdn, const void* sgate, const void* out, MoeShapes* S) {
+  if (!gate_up || !down) return fail(DFLASH_ERR_INVALID_ARGUMENT, "gate_up and down descriptors are required");
+  const int64_t E = gate_up->experts, I2 = gate_up->rows;
+  if (I2 <= 0 || I2 % 2) return fail(DFLASH_ERR_INVALID_ARGUMENT, "gate_up rows must be 2*I");
+  const int64_t I = I2 / 2;
+  if (int r = check_route_args(T, E, k)) return r;
+  if (H <= 0 || H % 512) return fail(DFLASH_ERR_UNSUPPORTED, "hidden_size must be a positive multiple of 512");
+  if (I % 512) return fail(DFLASH_ERR_UNSUPPORTED, "intermediate size must be a multiple of 512");
+  if (int r = check_w4(gate_up, "gate_up", E, 2 * I, H)) return r;
+  if (int r = check_w4(down, "down", E, H, I)) return r;
+  if (gate_up->group_size != down->group_size)
+    return fail(DFLASH_ERR_UNSUPPORTED, "gate_up and down must share one group_size");
+  const bool shared = sgu || sdn || sgate;
+  if (shared) {
+    if (!sgu || !sdn || !sgate)
+      return fail(DFLASH_ERR_INVALID_ARGUMENT, "shared expert needs shared_gate_up, shared_down and shared_gate_weight");
+    if (int r = check_w4(sgu, "shared_gate_up", 1, 2 * I, H)) return r;
+    if (int r = check_w4(sdn, "shared_down", 1, H, I)) return r;
+    if (sgu->group_size != gate_up->group_size || sdn->group_size != gate_up->group_size ||
+        sgu->scale_dtype != gate_up->scale_dtype || sdn->scale_dtype != down->scale_dtype)
+      return fail(DFLASH_ERR_UNSUPPORTED, "shared expert must use the routed banks' group_size and scale dtypes");
+    if (!aligned16(sgate)) return fail(DFLASH_ERR_INVALID_ARGUMENT, "shared_gate_weight not 16-byte aligned");
+  }
+  if (T > 0 && (!hidden || !out)) return fail(DFLASH_ERR_INVALID_ARGUMENT, "hidden and out are required");
+  if (!aligned16(hidden) || !aligned16(out)) return fail(DFLASH_ERR_INVALID_ARGUMENT, "hidden/out not 16-byte aligned");
+  *S = MoeShapes{T, H, I, E, k, gate_up->group_size, shared, gate_up->scale_dtype == DFLASH_DTYPE_F32,
+                 down->scale_dtype == DFLASH_DTYPE_F32};
+  return DFLASH_OK;
+}
+
+// Launch prep -> gate_up -> down -> combine for a routing already in place.
+int run_experts(const MoeShapes& S, const void* hidden, const float* topk_weights, const int32_t* perm,
+                const int32_t* inv, const int32_t* offsets, const int32_t* hit, const int32_t* meta,
+                const dflash_w4* gate_up, const dflash_w4* down, const dflash_w4* sgu, const dflash_w4* sdn,
+                const void* sgate, void* out, void* ws, const MoeLayout& L, hipStream_t stream) {
+  using namespace dflash;
+  const int T = static_cast<int>(S.T), H = static_cast<int>(S.H), I = static_cast<int>(S.I);
+  const int k = static_cast<int>(S.k), G = static_cast<int>(S.G);
+  uint16_t* x_il = at<uint16_t>(ws, L.x_il);
+  float* xneg = at<float>(ws, L.xneg);
+  float* gate = at<float>(ws, L.gate);
+  launch_prep(static_cast<const uint16_t*>(hidden), T, H, G, x_il, xneg,
+              S.shared ? static_cast<const uint16_t*>(sgate) : nullptr, gate, stream);
+  if (int r = launch_status("prep")) return r;
+
+  W4GemmParams p{};
+  p.perm = perm;
+  p.offsets = offsets;
+  p.hit = hit;
+  p.meta = meta;
+  p.top_k = k;
+  p.T = T;
+  p.has_shared = S.shared ? 1 : 0;
+  p.max_slots = static_cast<int>(std::min<int64_t>(S.E, S.T * S.k)) + p.has_shared;
+  p.G = G;
+
+  // gate_up: N = 2I rows over K = H, SiLU*up epilogue into h
+  p.w = static_cast<const uint8_t*>(gate_up->packed);
+  p.s = gate_up->scales;
+  p.w_shared = S.shared ? static_cast<const uint8_t*>(sgu->packed) : nullptr;
+  p.s_shared = S.shared ? sgu->scales : nullptr;
+  p.w_stride = 2 * S.I * S.H / 2;
+  p.s_stride = 2 * S.I * (S.H / S.G);
+  p.N = 2 * I;
+  p.K = H;
+  p.act = x_il;
+  p.act_neg = xneg;
+  p.out_bf16 = at<uint16_t>(ws, L.h);
+  p.out_part = at<float>(ws, L.hpart);
+  p.items_per_slot = I / 16;
+  launch_w4_gemm(kModeGateUp, S.gu_f32, p, stream);
+  if (int r = launch_status("gate_up")) return r;
+
+  // down: N = H rows over K = I, routing-weight epilogue into y
+  p.w = static_cast<const uint8_t*>(down->packed);
+  p.s = down->scales;
+  p.w_shared = S.shared ? static_cast<const uint8_t*>(sdn->packed) : nullptr;
+  p.s_shared = S.shared ? sdn->scales : nullptr;
+  p.w_stride = S.H * S.I / 2;
+  p.s_stride = S.H * (S.I / S.G);
+  p.N = H;
+  p.K = I;
+  p.act = at<uint16_t>(ws, L.h);
+  p.act_neg = at<float>(ws, L.hpart);
+  p.out_bf16 = nullptr;
+  p.out_part = nullptr;
+  p.out_f32 = at<float>(ws, L.y);
+  p.route_w = topk_weights;
+  p.shared_gate = gate;
+  p.items_per_slot = H / 32;
+  launch_w4_gemm(kModeDown, S.dn_f32, p, stream);
+  if (int r = launch_status("down")) return r;
+
+  launch_combine(at<float>(ws, L.y), inv, T, k, H, p.has_shared, static_cast<uint16_t*>(out), stream);
+  return launch_status("combine");
+}
+
+}  // namespace
+
+extern "C" {
+
+int dflash_abi_version(void) { return DFLASH_ABI_VERSION; }
+
+const char* dflash_last_error(void) { return g_last_error.c_str(); }
+
+size_t dflash_qlinear_workspace_bytes(int64_t m, int64_t k, int64_t group_size) {
+  if (m < 0 || k <= 0 || group_size <= 0) return 0;
+  Carver c;
+  c.take(2 * static_cast<size_t>(m) * k);
+  c.take(4 * static_cast<size_t>(m) * (k / group_size));
+  return c.off;
+}
+
+int dflash_qlinear_w4a16(const void* x, int64_t m, const dflash_w4* weight, void* y, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  try {
+    if (!weight) return fail(DFLASH_ERR_INVALID_ARGUMENT, "weight descriptor is NULL");
+    if (m < 0) return fail(DFLASH_ERR_INVALID_ARGUMENT, "m must be >= 0");
+    if (m > (1 << 24)) return fail(DFLASH_ERR_UNSUPPORTED, "m above 2^24 is not supported");
+    const int64_t N = weight->rows, K = weight->cols;
+    if (int r = check_w4(weight, "weight", 1, N, K)) return r;
+    if (N <= 0 || N % 32) return fail(DFLASH_ERR_UNSUPPORTED, "qlinear needs N % 32 == 0");
+    if (K <= 0 || K % 512) return fail(DFLASH_ERR_UNSUPPORTED, "qlinear needs K % 512 == 0");
+    if (m == 0) return DFLASH_OK;
+    if (!x || !y || !aligned16(x) || !aligned16(y)) return fail(DFLASH_ERR_INVALID_ARGUMENT, "x/y NULL or not 16-byte aligned");
+    const size_t need = dflash_qlinear_workspace_bytes(m, K, weight->group_size);
+    if (!workspace || workspace_bytes < need || !aligned16(workspace))
+      return fail(DFLASH_ERR_WORKSPACE, "qlinear workspace needs " + std::to_string(need) + " bytes");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    Carver c;
+    uint16_t* x_il = at<uint16_t>(workspace, c.take(2 * static_cast<size_t>(m) * K));
+    float* xneg = at<float>(workspace, c.take(4 * static_cast<size_t>(m) * (K / weight->group_size)));
+    dflash::launch_prep(static_cast<const uint16_t*>(x), static_cast<int>(m), static_cast<int>(K),
+                        static_cast<int>(weight->group_size), x_il, xneg, nullptr, nullptr, st);
+    if (int r = launch_status("prep")) return r;
+    dflash::W4GemmParams p{};
+    p.w = static_cast<const uint8_t*>(weight->packed);
+    p.s = weight->scales;
+    p.N = static_cast<int>(N);
+    p.K = static_cast<int>(K);
+    p.G = static_cast<int>(weight->group_size);
+    p.act = x_il;
+    p.act_neg = xneg;
+    p.out_bf16 = static_cast<uint16_t*>(y);
+    p.M = static_cast<int>(m);
+    p.items_per_slot = static_cast<int>(N / 32);
+    p.max_slots = 1;
+    dflash::launch_w4_gemm(dflash::kModeLinear, weight->scale_dtype == DFLASH_DTYPE_F32, p, st);
+    return launch_status("qlinear");
+  } catch (...) {
+    return fail(DFLASH_ERR_HIP, "unexpected host exception");
+  }
+}
+
+int dflash_router_logits(const void* hidden, int64_t tokens, int64_t hidden_size, const void* router_weight,
+                         int64_t experts, float* logits, void* stream) {
+  try {
+    if (tokens < 0 || experts <= 0 || experts > dflash::kMaxExperts)
+      return fail(DFLASH_ERR_INVALID_ARGUMENT, "router needs tokens >= 0 and experts in [1, 1024]");
+    if (hidden_size <= 0 || hidden_size % 256) return fail(DFLASH_ERR_UNSUPPORTED, "router needs hidden_size % 256 == 0");
+    if (tokens == 0) return DFLASH_OK;
+    if (!hidden || !router_weight || !logits || !aligned16(hidden) || !aligned16(router_weight))
+      return fail(DFLASH_ERR_INVALID_ARGUMENT, "router: NULL or misaligned pointer");
+    dflash::launch_router(static_cast<const uint16_t*>(hidden), static_cast<const uint16_t*>(router_weight), logits,
+                          static_cast<int>(tokens), static_cast<int>(experts), static_cast<int>(hidden_size),
+                          static_cast<hipStream_t>(stream));
+    return launch_status("router");
+  } catch (...) {
+    return fail(DFLASH_ERR_HIP, "unexpected host exception");
+  }
+}
+
+size_t dflash_moe_route_workspace_bytes(int64_t tokens, int64_t experts, int64_t top_k) {
+  (void)top_k;
+  if (tokens < 0 || experts <= 0) return 0;
+  return route_layout(tokens, experts).total;
+}
+
+int dflash_moe_route(const float* logits, int64_t tokens, int64_t experts, int64_t top_k, int32_t* topk_ids,
+                     float* topk_weights, int32_t* perm, int32_t* inv_perm, int32_t* expert_offsets, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  try {
+    if (int r = check_route_args(tokens, experts, top_k)) return r;
+    if (!expert_offsets) return fail(DFLASH_ERR_INVALID_ARGUMENT, "expert_offsets is required");
+    if (tokens > 0 && (!logits || !topk_ids || !topk_weights || !perm || !inv_perm))
+      return fail(DFLASH_ERR_INVALID_ARGUMENT, "route: NULL pointer");
+    const RouteLayout L = route_layout(tokens, experts);
+    if (!workspace || workspace_bytes < L.total || !aligned16(workspace))
+      return fail(DFLASH_ERR_WORKSPACE, "route workspace needs " + std::to_string(L.total) + " bytes");
+    dflash::launch_route(logits, static_cast<int>(tokens), static_cast<int>(experts), static_cast<int>(top_k), topk_ids,
+                         topk_weights, perm, inv_perm, expert_offsets, at<int32_t>(workspace, L.hit),
+                         at<int32_t>(workspace, L.meta), at<int32_t>(workspace, L.counts),
+                         at<uint32_t>(workspace, L.bitmap), true, static_cast<hipStream_t>(stream));
+    return launch_status("route");
+  } catch (...) {
+    return fail(DFLASH_ERR_HIP, "unexpected host exception");
+  }
+}
+
+size_t dflash_moe_workspace_bytes(int64_t tokens, int64_t hidden_size, int64_t inter_size, int64_t experts,
+                                  int64_t top_k, int64_t group_size, int has_shared) {
+  if (tokens < 0 || hidden_size <= 0 || inter_size <= 0 || experts <= 0 || top_k <= 0 || group_size <= 0) return 0;
+  return moe_layout(tokens, hidden_size, inter_size, experts, top_k, group_size, has_shared != 0).total;
+}
+
+int dflash_moe_experts_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, int64_t top_k,
+                             const float* topk_weights, const int32_t* perm, const int32_t* inv_perm,
+                             const int32_t* expert_offsets, const dflash_w4* gate_up, const dflash_w4* down,
+                             const dflash_w4* shared_gate_up, const dflash_w4* shared_down,
+                             const void* shared_gate_weight, void* out, void* workspace, size_t workspace_bytes,
+                             void* stream) {
+  try {
+    MoeShapes S;
+    if (int r = check_moe(hidden, tokens, hidden_size, top_k, gate_up, down, shared_gate_up, shared_down,
+                          shared_gate_weight, out, &S))
+      return r;
+    if (tokens == 0) return DFLASH_OK;
+    if (!topk_weights || !perm || !inv_perm || !expert_offsets)
+      return fail(DFLASH_ERR_INVALID_ARGUMENT, "experts: routing arrays are required");
+    const MoeLayout L = moe_layout(S.T, S.H, S.I, S.E, S.k, S.G, S.shared);
+    if (!workspace || workspace_bytes < L.total || !aligned16(workspace))
+      return fail(DFLASH_ERR_WORKSPACE, "moe workspace needs " + std::to_string(L.total) + " bytes");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    int32_t* hit = at<int32_t>(workspace, L.route.hit);
+    int32_t* meta = at<int32_t>(workspace, L.route.meta);
+    dflash::launch_hitlist(expert_offsets, static_cast<int>(S.E), hit, meta, st);
+    if (int r = launch_status("hitlist")) return r;
+    return run_experts(S, hidden, topk_weights, perm, inv_perm, expert_offsets, hit, meta, gate_up, down,
+                       shared_gate_up, shared_down, shared_gate_weight, out, workspace, L, st);
+  } catch (...) {
+    return fail(DFLASH_ERR_HIP, "unexpected host exception");
+  }
+}
+
+int dflash_moe_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, const float* router_logits,
+                     const void* router_weight, int64_t top_k, const dflash_w4* gate_up, const dflash_w4* down,
+                     const dflash_w4* shared_gate_up, const dflash_w4* shared_down, const void* shared_gate_weight,
+                     void* out, float* logits_out, int32_t* topk_ids, float* topk_weights, int32_t* perm,
+                     int32_t* inv_perm, int32_t* expert_offsets, void* workspace, size_t workspace_bytes,
+                     void* stream) {
+  try {
+    MoeShapes S;
+    if (int r = check_moe(hidden, tokens, hidden_size, top_k, gate_up, down, shared_gate_up, shared_down,
+                          shared_gate_weight, out, &S))
+      return r;
+    if (!router_logits && !router_weight)
+      return fail(DFLASH_ERR_INVALID_ARGUMENT, "either router_logits or router_weight is required");
+    if (!router_logits && !aligned16(router_weight))
+      return fail(DFLASH_ERR_INVALID_ARGUMENT, "router_weight not 16-byte aligned");
+    if (!expert_offsets) return fail(DFLASH_ERR_INVALID_ARGUMENT, "expert_offsets is required");
+    if (tokens > 0 && (!topk_ids || !topk_weights || !perm || !inv_perm))
+      return fail(DFLASH_ERR_INVALID_ARGUMENT, "routing output arrays are required");
+    const MoeLayout L = moe_layout(S.T, S.H, S.I, S.E, S.k, S.G, S.shared);
+    if (!workspace || workspace_bytes < L.total || !aligned16(workspace))
+      return fail(DFLASH_ERR_WORKSPACE, "moe workspace needs " + std::to_string(L.total) + " bytes");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const float* logits = router_logits;
+    if (!logits) {
+      float* dst = logits_out ? logits_out : at<float>(workspace, L.logits);
+      if (tokens > 0) {
+        dflash::launch_router(static_cast<const uint16_t*>(hidden), static_cast<const uint16_t*>(router_weight), dst,
+                              static_cast<int>(S.T), static_cast<int>(S.E), static_cast<int>(S.H), st);
+        if (int r = launch_status("router")) return r;
+      }
+      logits = dst;
+    }
+    int32_t* hit = at<int32_t>(workspace, L.route.hit);
+    int32_t* meta = at<int32_t>(workspace, L.route.meta);
+    dflash::launch_route(logits, static_cast<int>(S.T), static_cast<int>(S.E), static_cast<int>(S.k), topk_ids,
+                         topk_weights, perm, inv_perm, expert_offsets, hit, meta,
+                         at<int32_t>(workspace, L.route.counts), at<uint32_t>(workspace, L.route.bitmap), true, st);
+    if (int r = launch_status("route")) return r;
+    if (tokens == 0) return DFLASH_OK;
+    return run_experts(S, hidden, topk_weights, perm, inv_perm, expert_offsets, hit, meta, gate_up, down,
+                       shared_gate_up, shared_down, shared_gate_weight, out, workspace, L, st);
+  } catch (...) {
+    return fail(DFLASH_ERR_HIP, "unexpected host exception");
+  }
+}
+
+}  // extern "C"

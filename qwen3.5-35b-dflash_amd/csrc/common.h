@@ -1,0 +1,98 @@
+// Shared device helpers for the gfx950 W4A16 qlinear / routed-MoE kernels.
+//
+// Conventions used by every kernel in this library:
+//   * wave64; lane = threadIdx.x & 63.
+//   * v_mfma_f32_16x16x32_bf16 operand layout: lane l supplies row (l & 15) of
+//     A and column (l & 15) of B, each with 8 k-values from k-octet (l >> 4);
+//     the 4 fp32 results of lane l are D[4*(l>>4) + e][l & 15], e = 0..3.
+//   * Packed int4 weights are the portable K-packed format: uint8 [N][K/2],
+//     even k in the low nibble, signed two's complement.  One 32-bit word holds
+//     8 consecutive k.  dequant8() turns it into four bf16 pairs
+//     (k0,k4) (k1,k5) (k2,k6) (k3,k7), each value being 136 + q.
+//   * Activations feeding a W4 MFMA are therefore stored "octet-interleaved":
+//     within each block of 8 k the order is k0 k4 k1 k5 k2 k6 k3 k7, so one
+//     16-byte load gives the matching A operand.  The +136 offset is removed
+//     per group with the precomputed term -136 * sum_group(x) ("xneg").
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dflash {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kNibbleMask = 0x000F000Fu;
+constexpr uint32_t kBf16Magic = 0x43004300u;   // bf16 pair (128.0, 128.0)
+constexpr float kDequantOffset = 136.0f;       // 128 + 8 (sign flip of the nibble)
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bits) {
+  uint32_t d;
+  // gfx9 VOP3 reads at most one SGPR: mask from an SGPR, the magic bits from a VGPR.
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "s"(mask), "v"(bits));
+  return d;
+}
+
+// 8 signed nibbles -> 4 bf16 pairs holding 136+q in the octet-interleaved order.
+__device__ __forceinline__ uint4 dequant8(uint32_t w) {
+  w ^= 0x88888888u;
+  uint4 r;
+  r.x = and_or(w, kNibbleMask, kBf16Magic);
+  r.y = and_or(w >> 4, kNibbleMask, kBf16Magic);
+  r.z = and_or(w >> 8, kNibbleMask, kBf16Magic);
+  r.w = and_or(w >> 12, kNibbleMask, kBf16Magic);
+  return r;
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ f32x4 mfma16x16x32(uint4 a, uint4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 mfma16x16x4f32(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t v) {
+  return __uint_as_float(static_cast<uint32_t>(v) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (NaN stays NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+template <typename ScaleT>
+__device__ __forceinline__ float load_scale(const ScaleT* p);
+template <>
+__device__ __forceinline__ float load_scale<uint16_t>(const uint16_t* p) { return bf16_to_f32(*p); }
+template <>
+__device__ __forceinline__ float load_scale<float>(const float* p) { return *p; }
+
+// Interleaved position of column c inside its octet (k0 k4 k1 k5 k2 k6 k3 k7).
+__device__ __forceinline__ int octet_slot(int c) { return (c & ~7) | ((c & 3) << 1) | ((c >> 2) & 1); }
+
+// Sum over the 16 lanes that share (lane >> 4).
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __shfl_xor(v, 1, 64);
+  v += __shfl_xor(v, 2, 64);
+  v += __shfl_xor(v, 4, 64);
+  v += __shfl_xor(v, 8, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+
+}  // namespace dflash

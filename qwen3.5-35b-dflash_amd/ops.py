@@ -1,0 +1,224 @@
+"""PyTorch-ROCm wrappers over the C ABI of ``libdflash_hip.so``.
+
+Tensors must live on a ROCm device; every call is enqueued on the current
+torch stream of that device, allocates its outputs and workspace through
+torch, and raises :class:`DflashError` with the library's message on any
+nonzero status.  There is no CPU or dense fallback (reference policy,
+``model/qwen35_moe_dflash/fused/ops.py:133-135``).
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import NamedTuple, Optional
+
+import torch
+
+from . import _lib
+from .packing import PackedW4, SharedExpert
+
+
+class Routing(NamedTuple):
+    """Device routing of ``T`` tokens over ``E`` experts (see ``include/dflash_hip.h``)."""
+
+    ids: torch.Tensor        # int32 [T, k]
+    weights: torch.Tensor    # fp32 [T, k]
+    perm: torch.Tensor       # int32 [T*k]
+    inv: torch.Tensor        # int32 [T*k]
+    offsets: torch.Tensor    # int32 [E+1]
+
+
+def _require_device(*tensors) -> torch.device:
+    device = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+            raise ValueError("mi355x-hip operations require tensors on a ROCm device")
+        if device is None:
+            device = t.device
+        elif t.device != device:
+            raise ValueError("all tensors must be on the same device")
+    if device is None:
+        raise ValueError("no tensor given")
+    return device
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _desc(w: PackedW4) -> _lib.W4Desc:
+    return _lib.W4Desc(
+        packed=w.packed.data_ptr(), scales=w.scales.data_ptr(), experts=w.experts, rows=w.rows, cols=w.cols,
+        group_size=w.group_size,
+        scale_dtype=_lib.DTYPE_F32 if w.scales.dtype == torch.float32 else _lib.DTYPE_BF16)
+
+
+def _workspace(nbytes: int, device: torch.device, workspace: Optional[torch.Tensor]) -> torch.Tensor:
+    if workspace is not None:
+        if workspace.dtype != torch.uint8 or workspace.numel() < nbytes or workspace.device != device:
+            raise ValueError(f"workspace must be a uint8 tensor of at least {nbytes} bytes on {device}")
+        return workspace
+    return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+
+
+def qlinear(x: torch.Tensor, weight: PackedW4, *, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """W4A16 linear ``x[..., K] -> [..., N]`` (bf16 in, bf16 out, fp32 accumulation)."""
+    weight.validate("weight")
+    if weight.packed.ndim != 2:
+        raise ValueError("qlinear takes one packed matrix [N, K/2]")
+    device = _require_device(x, weight.packed)
+    if x.dtype != torch.bfloat16 or x.shape[-1] != weight.cols:
+        raise ValueError(f"x must be bfloat16 [..., {weight.cols}]")
+    flat = x.reshape(-1, weight.cols).contiguous()
+    m = flat.shape[0]
+    out = torch.empty((m, weight.rows), dtype=torch.bfloat16, device=device)
+    lib = _lib.load()
+    ws = _workspace(lib.dflash_qlinear_workspace_bytes(m, weight.cols, weight.group_size), device, workspace)
+    desc = _desc(weight)
+    _lib.call("dflash_qlinear_w4a16", _ptr(flat), m, ctypes.byref(desc), _ptr(out), _ptr(ws), ws.numel(),
+              _stream(device))
+    return out.reshape(*x.shape[:-1], weight.rows)
+
+
+def router_logits(hidden: torch.Tensor, router_weight: torch.Tensor) -> torch.Tensor:
+    """fp32 ``[T, E]`` logits from bf16 ``hidden [..., H]`` and bf16 ``router_weight [E, H]``."""
+    device = _require_device(hidden, router_weight)
+    if hidden.dtype != torch.bfloat16 or router_weight.dtype != torch.bfloat16:
+        raise ValueError("router needs bfloat16 hidden and router_weight")
+    if router_weight.ndim != 2 or router_weight.shape[1] != hidden.shape[-1]:
+        raise ValueError("router_weight must be [E, H]")
+    flat = hidden.reshape(-1, hidden.shape[-1]).contiguous()
+    w = router_weight.contiguous()
+    logits = torch.empty((flat.shape[0], w.shape[0]), dtype=torch.float32, device=device)
+    _lib.call("dflash_router_logits", _ptr(flat), flat.shape[0], flat.shape[1], _ptr(w), w.shape[0], _ptr(logits),
+              _stream(device))
+    return logits
+
+
+def _routing_buffers(t: int, e: int, k: int, device) -> Routing:
+    return Routing(
+        ids=torch.empty((t, k), dtype=torch.int32, device=device),
+        weights=torch.empty((t, k), dtype=torch.float32, device=device),
+        perm=torch.empty((t * k,), dtype=torch.int32, device=device),
+        inv=torch.empty((t * k,), dtype=torch.int32, device=device),
+        offsets=torch.empty((e + 1,), dtype=torch.int32, device=device))
+
+
+def route(logits: torch.Tensor, top_k: int, *, workspace: Optional[torch.Tensor] = None) -> Routing:
+    """Top-k routing and stable expert permutation from fp32 logits ``[T, E]``."""
+    device = _require_device(logits)
+    if logits.dtype != torch.float32 or logits.ndim != 2:
+        raise ValueError("router logits must be float32 [T, E]")
+    if type(top_k) is not int:
+        raise ValueError("top_k must be an int")
+    logits = logits.contiguous()
+    t, e = logits.shape
+    r = _routing_buffers(t, e, top_k, device)
+    lib = _lib.load()
+    ws = _workspace(lib.dflash_moe_route_workspace_bytes(t, e, top_k), device, workspace)
+    _lib.call("dflash_moe_route", _ptr(logits), t, e, top_k, _ptr(r.ids), _ptr(r.weights), _ptr(r.perm),
+              _ptr(r.inv), _ptr(r.offsets), _ptr(ws), ws.numel(), _stream(device))
+    return r
+
+
+def _shared_args(shared: Optional[SharedExpert]):
+    if shared is None:
+        return None, None, None, None
+    if not isinstance(shared, SharedExpert):
+        raise ValueError("shared must be a SharedExpert")
+    shared.gate_up.validate("shared.gate_up")
+    shared.down.validate("shared.down")
+    gw = shared.gate_weight
+    if gw.dtype != torch.bfloat16:
+        raise ValueError("shared.gate_weight must be bfloat16 [H]")
+    gw = gw.reshape(-1).contiguous()
+    return _desc(shared.gate_up), _desc(shared.down), gw, (shared.gate_up.packed, shared.down.packed)
+
+
+def _moe_common(hidden, gate_up: PackedW4, down: PackedW4, shared):
+    gate_up.validate("gate_up")
+    down.validate("down")
+    if gate_up.packed.ndim != 3 or down.packed.ndim != 3:
+        raise ValueError("expert banks must be [E, N, K/2]")
+    device = _require_device(hidden, gate_up.packed, down.packed)
+    if hidden.dtype != torch.bfloat16:
+        raise ValueError("hidden must be bfloat16")
+    h = hidden.shape[-1]
+    flat = hidden.reshape(-1, h).contiguous()
+    sgu, sdn, sgate, keep = _shared_args(shared)
+    if keep is not None:
+        _require_device(hidden, *keep, sgate)
+    return device, flat, sgu, sdn, sgate
+
+
+def moe_experts(hidden: torch.Tensor, routing: Routing, gate_up: PackedW4, down: PackedW4, *,
+                shared: Optional[SharedExpert] = None, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Expert FFN + combine for a given routing; bf16 ``[T, H]``."""
+    device, flat, sgu, sdn, sgate = _moe_common(hidden, gate_up, down, shared)
+    t, h = flat.shape
+    k = routing.ids.shape[1] if routing.ids.ndim == 2 else 0
+    out = torch.empty_like(flat)
+    lib = _lib.load()
+    ws = _workspace(lib.dflash_moe_workspace_bytes(t, h, gate_up.rows // 2, gate_up.experts, k, gate_up.group_size,
+                                                   int(shared is not None)), device, workspace)
+    gu, dn = _desc(gate_up), _desc(down)
+    _lib.call("dflash_moe_experts_w4a16", _ptr(flat), t, h, k, _ptr(routing.weights.contiguous()),
+              _ptr(routing.perm), _ptr(routing.inv), _ptr(routing.offsets), ctypes.byref(gu), ctypes.byref(dn),
+              None if sgu is None else ctypes.byref(sgu), None if sdn is None else ctypes.byref(sdn), _ptr(sgate),
+              _ptr(out), _ptr(ws), ws.numel(), _stream(device))
+    return out
+
+
+def moe_w4a16(hidden: torch.Tensor, gate_up: PackedW4, down: PackedW4, *, top_k: int,
+              router_weight: Optional[torch.Tensor] = None, router_logits: Optional[torch.Tensor] = None,
+              shared: Optional[SharedExpert] = None, workspace: Optional[torch.Tensor] = None,
+              return_routing: bool = False):
+    """Whole routed-MoE layer (+ optional shared expert) on packed banks; bf16 ``[T, H]``.
+
+    With ``return_routing=True`` also returns ``(Routing, logits)``; ``logits``
+    are the fp32 router logits the routing was computed from.
+    """
+    device, flat, sgu, sdn, sgate = _moe_common(hidden, gate_up, down, shared)
+    if type(top_k) is not int:
+        raise ValueError("top_k must be an int")
+    t, h = flat.shape
+    e = gate_up.experts
+    if router_logits is not None:
+        _require_device(router_logits)
+        if router_logits.dtype != torch.float32 or tuple(router_logits.shape) != (t, e):
+            raise ValueError(f"router_logits must be float32 [{t}, {e}]")
+        logits_in = router_logits.contiguous()
+        logits_out = logits_in
+    else:
+        if router_weight is None:
+            raise ValueError("router_weight or router_logits is required")
+        _require_device(router_weight)
+        if router_weight.dtype != torch.bfloat16 or tuple(router_weight.shape) != (e, h):
+            raise ValueError(f"router_weight must be bfloat16 [{e}, {h}]")
+        logits_in = None
+        logits_out = torch.empty((t, e), dtype=torch.float32, device=device)
+    rw = None if router_weight is None else router_weight.contiguous()
+    r = _routing_buffers(t, e, top_k, device)
+    out = torch.empty_like(flat)
+    lib = _lib.load()
+    ws = _workspace(lib.dflash_moe_workspace_bytes(t, h, gate_up.rows // 2, e, top_k, gate_up.group_size,
+                                                   int(shared is not None)), device, workspace)
+    gu, dn = _desc(gate_up), _desc(down)
+    _lib.call("dflash_moe_w4a16", _ptr(flat), t, h, _ptr(logits_in), _ptr(rw), top_k, ctypes.byref(gu),
+              ctypes.byref(dn), None if sgu is None else ctypes.byref(sgu), None if sdn is None else ctypes.byref(sdn),
+              _ptr(sgate), _ptr(out), _ptr(logits_out if logits_in is None else None), _ptr(r.ids), _ptr(r.weights),
+              _ptr(r.perm), _ptr(r.inv), _ptr(r.offsets), _ptr(ws), ws.numel(), _stream(device))
+    if return_routing:
+        return out, r, logits_out
+    return out
+
+
+def moe_workspace_bytes(tokens: int, hidden: int, inter: int, experts: int, top_k: int, group_size: int,
+                        has_shared: bool) -> int:
+    return int(_lib.load().dflash_moe_workspace_bytes(tokens, hidden, inter, experts, top_k, group_size,
+                                                      int(has_shared)))
