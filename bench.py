@@ -1,0 +1,257 @@
+"""Benchmark: one routed-MoE layer (W4A16, g128) of the verify block on one MI355X.
+
+Step = one whole MoE layer forward at T=16 tokens (router logits, top-8
+routing and permutation, grouped gate/up + SiLU*up, down, weighted combine,
+gated shared expert) through ``dflash_moe_w4a16``.  Inputs are resident in
+HBM before timing.  Three independent weight sets (~1.25 GB) and eight hidden
+blocks are rotated so that the 256 MB Infinity Cache cannot serve the
+~167 MB per-step working set.
+
+Steps are replayed from HIP graphs (24 layer-steps per graph, the way a
+multi-layer verify forward would be issued), so host launch overhead is not
+part of the measurement.
+
+Prints ONE JSON line.  ``value`` is microseconds per MoE layer (lower is
+better).  ``roofline`` is the expert stage (the kernels that stream the int4
+expert weights), timed with HIP events on the launch stream:
+achieved = int4 weight bytes of the hit experts + shared expert / time.
+``prefill`` reports the T=2048 layer in TFLOP/s against bf16 MFMA peak.
+``cpu_baseline`` times the oracle's CPU restatement of the same layer.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+PKG_DIR = ROOT / "qwen3.5-35b-dflash_amd"
+PKG_NAME = "qwen35_dflash_amd"
+
+METRIC = "µs per MoE layer at T=16 verify (HBM GB/s %); TFLOP/s at T=2048 prefill"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2516.6
+INT4_BYTES_PER_EXPERT = 2 * 512 * 2048 // 2 + 2048 * 512 // 2        # gate_up + down, packed int4
+SCALE_BYTES_PER_EXPERT = (2 * 512 * 2048 // 128 + 2048 * 512 // 128) * 2  # bf16 group-128 scales
+
+
+def load_package():
+    if PKG_NAME in sys.modules:
+        return sys.modules[PKG_NAME]
+    spec = importlib.util.spec_from_file_location(PKG_NAME, PKG_DIR / "__init__.py",
+                                                  submodule_search_locations=[str(PKG_DIR)])
+    module = importlib.util.module_from_spec(spec)
+    sys.modules[PKG_NAME] = module
+    spec.loader.exec_module(module)
+    return module
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def device_bank(pkg, gen, shape, device):
+    """Random packed int4 bank generated on the device (uniform bytes = two uniform int4)."""
+    packed = torch.randint(0, 256, (*shape[:-1], shape[-1] // 2), dtype=torch.uint8, device=device, generator=gen)
+    scales = (torch.rand((*shape[:-1], shape[-1] // 128), device=device, generator=gen) * 0.015 + 0.005)
+    return pkg.PackedW4(packed, scales.to(torch.bfloat16).contiguous(), 128)
+
+
+def weight_sets(pkg, nsets, device, seed=1234, hidden=2048, inter=512, experts=256):
+    gen = torch.Generator(device=device).manual_seed(seed)
+    sets = []
+    for _ in range(nsets):
+        gu = device_bank(pkg, gen, (experts, 2 * inter, hidden), device)
+        dn = device_bank(pkg, gen, (experts, hidden, inter), device)
+        sh = pkg.SharedExpert(device_bank(pkg, gen, (2 * inter, hidden), device),
+                              device_bank(pkg, gen, (hidden, inter), device),
+                              (torch.randn((hidden,), device=device, generator=gen) * 0.02).to(torch.bfloat16))
+        router = (torch.randn((experts, hidden), device=device, generator=gen) * 0.02).to(torch.bfloat16)
+        sets.append((gu, dn, sh, router))
+    return sets
+
+
+def moe_flops(tokens, k, hidden=2048, inter=512):
+    per_row = 2 * (2 * inter * hidden + hidden * inter)
+    return per_row * (tokens * k + tokens)
+
+
+def _graph(fn, length):
+    """Capture `length` consecutive steps fn(0..length-1) into one HIP graph."""
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for j in range(length):      # eager pass: warms up and settles the graph's allocations
+            fn(j)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for j in range(length):
+            fn(j)
+    torch.cuda.synchronize()
+    return graph
+
+
+def time_steps(fn, steps, warmup, period=24):
+    """Time exactly `steps` steps, replayed from HIP graphs of `period` steps, with HIP events."""
+    full, rest = divmod(steps, period)
+    main = _graph(fn, period) if full else None
+    tail = _graph(fn, rest) if rest else None
+    for _ in range(max(1, warmup // period)):
+        (main or tail).replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(full):
+        main.replay()
+    if tail is not None:
+        tail.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
+def time_layer(pkg, sets, blocks, top_k, steps, warmup, workspace):
+    """Whole-layer time per step; step j uses weight set j % sets and hidden block j % blocks."""
+    def step(j):
+        gu, dn, sh, router = sets[j % len(sets)]
+        pkg.ops.moe_w4a16(blocks[j % len(blocks)], gu, dn, top_k=top_k, router_weight=router, shared=sh,
+                          workspace=workspace)
+    return time_steps(step, steps, warmup)
+
+
+def time_experts(pkg, sets, blocks, top_k, steps, warmup, workspace):
+    """Expert-stage time per step (routing prepared beforehand) and the mean hit-expert count."""
+    period = 24
+    prepared = []
+    for j in range(period):
+        gu, dn, sh, router = sets[j % len(sets)]
+        x = blocks[j % len(blocks)]
+        r = pkg.ops.route(pkg.ops.router_logits(x, router), top_k)
+        hit = int((r.offsets[1:] > r.offsets[:-1]).sum().item())
+        prepared.append((x, r, gu, dn, sh, hit))
+    torch.cuda.synchronize()
+
+    def step(j):
+        x, r, gu, dn, sh, _ = prepared[j % period]
+        pkg.ops.moe_experts(x, r, gu, dn, shared=sh, workspace=workspace)
+    ms = time_steps(step, steps, warmup, period)
+    return ms, statistics.mean(p[5] for p in prepared)
+
+
+def cpu_baseline(pkg, tokens, top_k, seconds_budget=20.0):
+    """Oracle CPU restatement of the same layer (dense bf16 banks of the hit experts), median of timed runs."""
+    import numpy as np
+    from oracle import moe as oracle_moe, routing as oracle_routing, w4 as oracle_w4
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", min(16, os.cpu_count() or 1)))
+    torch.set_num_threads(threads)
+    layer = pkg.synthetic.moe_layer(tokens, seed=0)
+    logits = oracle_moe.router_logits(layer.hidden, layer.router_weight)
+    ids, _ = oracle_routing.topk(logits, top_k)
+    hit = np.unique(ids).tolist()
+    e, i2, h = layer.gate_up.experts, layer.gate_up.rows, layer.gate_up.cols
+    # dense bf16 banks (the reference's input contract), dequantised outside the timed region;
+    # only hit experts are materialised, the others stay zero (never read)
+    gate_up = torch.zeros((e, i2, h), dtype=torch.bfloat16)
+    down = torch.zeros((e, h, i2 // 2), dtype=torch.bfloat16)
+    for ex in hit:
+        gate_up[ex] = torch.from_numpy(oracle_w4.dequantize(layer.gate_up.packed[ex].numpy(),
+                                                            layer.gate_up.scales[ex], 128)).to(torch.bfloat16)
+        down[ex] = torch.from_numpy(oracle_w4.dequantize(layer.down.packed[ex].numpy(),
+                                                         layer.down.scales[ex], 128)).to(torch.bfloat16)
+    run = lambda: oracle_moe.moe_dense(layer.hidden, logits, top_k, gate_up, down)  # noqa: E731
+    times = []
+    t_start = time.perf_counter()
+    for i in range(13):
+        t0 = time.perf_counter()
+        run()
+        if i >= 3:
+            times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > seconds_budget and len(times) >= 3:
+            break
+    med = statistics.median(times)
+    return {"value": round(med * 1e6, 1), "unit": "us/layer", "cores": threads, "kind": "port",
+            "sample": f"oracle.moe.moe_dense, T={tokens} routed experts (dense bf16 banks of the {len(hit)} hit "
+                      f"experts dequantised beforehand, shared expert not included), median of {len(times)} runs "
+                      f"after 3 warmups, torch CPU threads={threads}"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--sets", type=int, default=3, help="independent weight sets rotated per step")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (the MoE layer would shard by "
+              "expert parallelism, see DESIGN.md)", file=sys.stderr)
+        return 2
+    pkg = load_package()
+    assert torch.cuda.is_available(), "bench.py needs a ROCm device"
+    device = torch.device("cuda:0")
+    pkg._lib.load()
+    top_k, tokens = 8, 16
+
+    log("generating weight sets on the device")
+    sets = weight_sets(pkg, args.sets, device)
+    gen = torch.Generator(device=device).manual_seed(99)
+    blocks = [torch.randn((tokens, 2048), device=device, generator=gen).to(torch.bfloat16) for _ in range(8)]
+    ws = torch.empty(pkg.ops.moe_workspace_bytes(2048, 2048, 512, 256, top_k, 128, True), dtype=torch.uint8,
+                     device=device)
+
+    log("timing the T=16 layer")
+    ms = time_layer(pkg, sets, blocks, top_k, args.steps, args.warmup, ws)
+    log("timing the expert stage")
+    exp_ms, hits = time_experts(pkg, sets, blocks, top_k, args.steps, args.warmup, ws)
+    int4_bytes = (hits + 1) * INT4_BYTES_PER_EXPERT
+    all_bytes = (hits + 1) * (INT4_BYTES_PER_EXPERT + SCALE_BYTES_PER_EXPERT)
+    achieved = int4_bytes / (exp_ms * 1e-3) / 1e9
+    layer_gbs = int4_bytes / (ms * 1e-3) / 1e9
+
+    result = {
+        "metric": METRIC, "value": round(ms * 1e3, 2), "unit": "us/layer", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded; int4 weights uniform in [-8,7], bf16 group-128 scales U(0.005,0.02), "
+                "activations N(0,1); 3 rotated weight sets)",
+        "config": {"workload": "routed MoE layer, DFlash verify block: T=16, H=2048, I=512, 256 experts top-8 "
+                               "+ shared expert, W4A16 group 128, router included",
+                   "tokens": tokens, "hidden": 2048, "inter": 512, "experts": 256, "top_k": top_k,
+                   "group_size": 128, "weight_sets": args.sets},
+        "layer_int4_gbs": round(layer_gbs, 1),
+        "layer_hbm_frac_int4": round(layer_gbs / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "expert stage (prep, hitlist, w4_gemm gate_up, w4_gemm down, combine)",
+                     "stage_us": round(exp_ms * 1e3, 2), "hit_experts_mean": round(hits, 2),
+                     "int4_bytes_per_launch": int(int4_bytes), "all_weight_bytes_per_launch": int(all_bytes)},
+    }
+    if not args.no_prefill:
+        log("timing the T=2048 prefill layer")
+        blocks_p = [torch.randn((2048, 2048), device=device, generator=gen).to(torch.bfloat16) for _ in range(2)]
+        steps_p = max(5, args.steps // 10)
+        ms_p = time_layer(pkg, sets, blocks_p, top_k, steps_p, max(2, args.warmup // 10), ws)
+        tflops = moe_flops(2048, top_k) / (ms_p * 1e-3) / 1e12
+        result["prefill"] = {"tokens": 2048, "us_per_layer": round(ms_p * 1e3, 1), "tflops": round(tflops, 2),
+                             "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4), "steps": steps_p}
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline")
+        result["cpu_baseline"] = cpu_baseline(pkg, tokens, top_k)
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -4,6 +4,7 @@
 // workspace, and enqueues kernels on the caller's stream.  No allocation, no
 // synchronisation, no C++ exception crosses the ABI.
 #include <algorithm>
+#include <atomic>
 #include <string>
 
 #include "../../include/dflash_hip.h"
@@ -59,16 +60,21 @@ int check_w4(const dflash_w4* w, const char* name, int64_t experts, int64_t rows
 
 // ---------------------------------------------------------------- layouts
 struct RouteLayout {
-  size_t meta, hit, counts, bitmap, total;
+  size_t meta, hit, pass_start, slot_table, pass_slot, counts, slotmap, total;
 };
 
-RouteLayout route_layout(int64_t T, int64_t E) {
+RouteLayout route_layout(int64_t T, int64_t k, int64_t E) {
   Carver c;
   RouteLayout L;
   L.meta = c.take(16);
-  L.hit = c.take(4 * static_cast<size_t>(E));
-  L.counts = c.take(4 * static_cast<size_t>(E));
-  L.bitmap = c.take(4 * static_cast<size_t>(T) * ((E + 31) / 32));
+  L.hit = c.take(4 * static_cast<size_t>(E + 1));
+  L.pass_start = c.take(4 * static_cast<size_t>(E + 4));
+  L.slot_table = c.take(16 * static_cast<size_t>(E + 2));
+  L.pass_slot = c.take(4 * static_cast<size_t>(T * k + T + 4));  // a pass holds at least one row
+  // counts and the slot map are contiguous: one clearing pass covers both
+  L.counts = c.off;
+  L.slotmap = L.counts + 4 * static_cast<size_t>(E);
+  c.take(4 * static_cast<size_t>(E) + static_cast<size_t>(E) * T + 4);
   L.total = c.off;
   return L;
 }
@@ -78,15 +84,15 @@ struct MoeLayout {
   size_t logits, x_il, xneg, gate, h, hpart, y, total;
 };
 
-MoeLayout moe_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int64_t G, bool shared) {
+MoeLayout moe_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, bool shared) {
   MoeLayout L;
-  L.route = route_layout(T, E);
+  L.route = route_layout(T, k, E);
   Carver c;
   c.off = L.route.total;
   const size_t rows = static_cast<size_t>(T) * k + (shared ? T : 0);
   L.logits = c.take(4 * static_cast<size_t>(T) * E);
   L.x_il = c.take(2 * static_cast<size_t>(T) * H);
-  L.xneg = c.take(4 * static_cast<size_t>(T) * (H / G));
+  L.xneg = c.take(4 * static_cast<size_t>(T) * (H / 128));
   L.gate = c.take(4 * static_cast<size_t>(T));
   L.h = c.take(2 * rows * I);
   L.hpart = c.take(4 * rows * (I / 16));
@@ -99,6 +105,20 @@ template <typename T>
 T* at(void* base, size_t off) {
   return reinterpret_cast<T*>(static_cast<char*>(base) + off);
 }
+
+// Compute units of the current device (persistent grids launch one workgroup per CU).
+int cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+  cache[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+int token_tiles(int64_t T) { return T <= 16 ? 1 : 2; }
 
 int check_route_args(int64_t T, int64_t E, int64_t k) {
   if (T < 0) return fail(DFLASH_ERR_INVALID_ARGUMENT, "tokens must be >= 0");
@@ -126,17 +146,15 @@ int check_moe(const void* hidden, int64_t T, int64_t H, int64_t k, const dflash_
   if (I % 512) return fail(DFLASH_ERR_UNSUPPORTED, "intermediate size must be a multiple of 512");
   if (int r = check_w4(gate_up, "gate_up", E, 2 * I, H)) return r;
   if (int r = check_w4(down, "down", E, H, I)) return r;
-  if (gate_up->group_size != down->group_size)
-    return fail(DFLASH_ERR_UNSUPPORTED, "gate_up and down must share one group_size");
   const bool shared = sgu || sdn || sgate;
   if (shared) {
     if (!sgu || !sdn || !sgate)
       return fail(DFLASH_ERR_INVALID_ARGUMENT, "shared expert needs shared_gate_up, shared_down and shared_gate_weight");
     if (int r = check_w4(sgu, "shared_gate_up", 1, 2 * I, H)) return r;
     if (int r = check_w4(sdn, "shared_down", 1, H, I)) return r;
-    if (sgu->group_size != gate_up->group_size || sdn->group_size != gate_up->group_size ||
+    if (sgu->group_size != gate_up->group_size || sdn->group_size != down->group_size ||
         sgu->scale_dtype != gate_up->scale_dtype || sdn->scale_dtype != down->scale_dtype)
-      return fail(DFLASH_ERR_UNSUPPORTED, "shared expert must use the routed banks' group_size and scale dtypes");
+      return fail(DFLASH_ERR_UNSUPPORTED, "shared expert must use the routed banks' group sizes and scale dtypes");
     if (!aligned16(sgate)) return fail(DFLASH_ERR_INVALID_ARGUMENT, "shared_gate_weight not 16-byte aligned");
   }
   if (T > 0 && (!hidden || !out)) return fail(DFLASH_ERR_INVALID_ARGUMENT, "hidden and out are required");
@@ -146,47 +164,59 @@ int check_moe(const void* hidden, int64_t T, int64_t H, int64_t k, const dflash_
   return DFLASH_OK;
 }
 
-// Launch prep -> gate_up -> down -> combine for a routing already in place.
-int run_experts(const MoeShapes& S, const void* hidden, const float* topk_weights, const int32_t* perm,
-                const int32_t* inv, const int32_t* offsets, const int32_t* hit, const int32_t* meta,
-                const dflash_w4* gate_up, const dflash_w4* down, const dflash_w4* sgu, const dflash_w4* sdn,
-                const void* sgate, void* out, void* ws, const MoeLayout& L, hipStream_t stream) {
+// One W4 GEMM over the work table: the streaming kernel when it splits this K
+// evenly, the per-wave kernel otherwise.
+void launch_w4(int mode, bool fp32_scales, int mt, int max_slots, dflash::W4StreamParams& p, hipStream_t stream) {
+  using namespace dflash;
+  const int cols = mode == kModeGateUp ? p.N / 2 / 16 : p.N / 32;  // 16-column pairs or 32-row strips
+  const int rg = w4_stream_row_groups(p.K);
+  if (w4_stream_supports(p.K, p.G) && cols % rg == 0) {
+    p.strips = cols / rg;
+    launch_w4_stream(mode, fp32_scales, mt, cu_count(), p, stream);
+  } else {
+    launch_w4_gemm(mode, fp32_scales, max_slots, p, stream);
+  }
+}
+
+// gate_up -> down -> combine for a routing and work table already in place.
+int run_experts(const MoeShapes& S, const float* topk_weights, const int32_t* perm, const int32_t* inv,
+                const int32_t* offsets, const int32_t* hit, const int32_t* pass_start, const int32_t* meta,
+                const int4* slot_table, const int32_t* pass_slot, const dflash_w4* gate_up, const dflash_w4* down, const dflash_w4* sgu, const dflash_w4* sdn,
+                void* out, void* ws, const MoeLayout& L, hipStream_t stream) {
   using namespace dflash;
   const int T = static_cast<int>(S.T), H = static_cast<int>(S.H), I = static_cast<int>(S.I);
-  const int k = static_cast<int>(S.k), G = static_cast<int>(S.G);
-  uint16_t* x_il = at<uint16_t>(ws, L.x_il);
-  float* xneg = at<float>(ws, L.xneg);
-  float* gate = at<float>(ws, L.gate);
-  launch_prep(static_cast<const uint16_t*>(hidden), T, H, G, x_il, xneg,
-              S.shared ? static_cast<const uint16_t*>(sgate) : nullptr, gate, stream);
-  if (int r = launch_status("prep")) return r;
-
-  W4GemmParams p{};
+  const int k = static_cast<int>(S.k);
+  const int mt = token_tiles(S.T);
+  W4StreamParams p{};
   p.perm = perm;
   p.offsets = offsets;
   p.hit = hit;
+  p.pass_start = pass_start;
   p.meta = meta;
+  p.slot_table = slot_table;
+  p.pass_slot = pass_slot;
   p.top_k = k;
   p.T = T;
   p.has_shared = S.shared ? 1 : 0;
-  p.max_slots = static_cast<int>(std::min<int64_t>(S.E, S.T * S.k)) + p.has_shared;
-  p.G = G;
+  p.rows_per_pass = 16 * mt;
+  const int max_slots = static_cast<int>(std::min<int64_t>(S.E, S.T * S.k)) + p.has_shared;
 
   // gate_up: N = 2I rows over K = H, SiLU*up epilogue into h
   p.w = static_cast<const uint8_t*>(gate_up->packed);
   p.s = gate_up->scales;
   p.w_shared = S.shared ? static_cast<const uint8_t*>(sgu->packed) : nullptr;
   p.s_shared = S.shared ? sgu->scales : nullptr;
-  p.w_stride = 2 * S.I * S.H / 2;
-  p.s_stride = 2 * S.I * (S.H / S.G);
+  p.w_stride = S.I * S.H;
+  p.s_stride = 2 * S.I * (S.H / gate_up->group_size);
   p.N = 2 * I;
   p.K = H;
-  p.act = x_il;
-  p.act_neg = xneg;
+  p.G = static_cast<int>(gate_up->group_size);
+  p.act = at<uint16_t>(ws, L.x_il);
+  p.act_neg = at<float>(ws, L.xneg);
+  p.neg_parts = 1;
   p.out_bf16 = at<uint16_t>(ws, L.h);
   p.out_part = at<float>(ws, L.hpart);
-  p.items_per_slot = I / 16;
-  launch_w4_gemm(kModeGateUp, S.gu_f32, p, stream);
+  launch_w4(kModeGateUp, S.gu_f32, mt, max_slots, p, stream);
   if (int r = launch_status("gate_up")) return r;
 
   // down: N = H rows over K = I, routing-weight epilogue into y
@@ -195,22 +225,48 @@ int run_experts(const MoeShapes& S, const void* hidden, const float* topk_weight
   p.w_shared = S.shared ? static_cast<const uint8_t*>(sdn->packed) : nullptr;
   p.s_shared = S.shared ? sdn->scales : nullptr;
   p.w_stride = S.H * S.I / 2;
-  p.s_stride = S.H * (S.I / S.G);
+  p.s_stride = S.H * (S.I / down->group_size);
   p.N = H;
   p.K = I;
+  p.G = static_cast<int>(down->group_size);
   p.act = at<uint16_t>(ws, L.h);
   p.act_neg = at<float>(ws, L.hpart);
+  p.neg_parts = 8;
   p.out_bf16 = nullptr;
   p.out_part = nullptr;
   p.out_f32 = at<float>(ws, L.y);
   p.route_w = topk_weights;
-  p.shared_gate = gate;
-  p.items_per_slot = H / 32;
-  launch_w4_gemm(kModeDown, S.dn_f32, p, stream);
+  p.shared_gate = at<float>(ws, L.gate);
+  launch_w4(kModeDown, S.dn_f32, mt, max_slots, p, stream);
   if (int r = launch_status("down")) return r;
 
   launch_combine(at<float>(ws, L.y), inv, T, k, H, p.has_shared, static_cast<uint16_t*>(out), stream);
   return launch_status("combine");
+}
+
+dflash::RouteParams route_params(const float* logits, int64_t T, int64_t E, int64_t k, int32_t* ids, float* wts,
+                                 int32_t* perm, int32_t* inv, int32_t* offsets, void* ws, const RouteLayout& L,
+                                 int rows_per_pass, bool shared) {
+  dflash::RouteParams r{};
+  r.logits = logits;
+  r.T = static_cast<int>(T);
+  r.E = static_cast<int>(E);
+  r.k = static_cast<int>(k);
+  r.ids = ids;
+  r.wts = wts;
+  r.perm = perm;
+  r.inv = inv;
+  r.offsets = offsets;
+  r.hit = at<int32_t>(ws, L.hit);
+  r.pass_start = at<int32_t>(ws, L.pass_start);
+  r.meta = at<int32_t>(ws, L.meta);
+  r.counts = at<int32_t>(ws, L.counts);
+  r.slotmap = at<uint8_t>(ws, L.slotmap);
+  r.slot_table = at<int4>(ws, L.slot_table);
+  r.pass_slot = at<int32_t>(ws, L.pass_slot);
+  r.rows_per_pass = rows_per_pass;
+  r.has_shared = shared ? 1 : 0;
+  return r;
 }
 
 }  // namespace
@@ -225,7 +281,7 @@ size_t dflash_qlinear_workspace_bytes(int64_t m, int64_t k, int64_t group_size) 
   if (m < 0 || k <= 0 || group_size <= 0) return 0;
   Carver c;
   c.take(2 * static_cast<size_t>(m) * k);
-  c.take(4 * static_cast<size_t>(m) * (k / group_size));
+  c.take(4 * static_cast<size_t>(m) * (k / 128));
   return c.off;
 }
 
@@ -247,11 +303,17 @@ int dflash_qlinear_w4a16(const void* x, int64_t m, const dflash_w4* weight, void
     hipStream_t st = static_cast<hipStream_t>(stream);
     Carver c;
     uint16_t* x_il = at<uint16_t>(workspace, c.take(2 * static_cast<size_t>(m) * K));
-    float* xneg = at<float>(workspace, c.take(4 * static_cast<size_t>(m) * (K / weight->group_size)));
-    dflash::launch_prep(static_cast<const uint16_t*>(x), static_cast<int>(m), static_cast<int>(K),
-                        static_cast<int>(weight->group_size), x_il, xneg, nullptr, nullptr, st);
+    float* xneg = at<float>(workspace, c.take(4 * static_cast<size_t>(m) * (K / 128)));
+    dflash::FrontParams f{};
+    f.x = static_cast<const uint16_t*>(x);
+    f.T = static_cast<int>(m);
+    f.prep_rows = static_cast<int>(m);
+    f.H = static_cast<int>(K);
+    f.x_il = x_il;
+    f.xneg = xneg;
+    dflash::launch_front(f, st);
     if (int r = launch_status("prep")) return r;
-    dflash::W4GemmParams p{};
+    dflash::W4StreamParams p{};
     p.w = static_cast<const uint8_t*>(weight->packed);
     p.s = weight->scales;
     p.N = static_cast<int>(N);
@@ -259,11 +321,12 @@ int dflash_qlinear_w4a16(const void* x, int64_t m, const dflash_w4* weight, void
     p.G = static_cast<int>(weight->group_size);
     p.act = x_il;
     p.act_neg = xneg;
+    p.neg_parts = 1;
     p.out_bf16 = static_cast<uint16_t*>(y);
     p.M = static_cast<int>(m);
-    p.items_per_slot = static_cast<int>(N / 32);
-    p.max_slots = 1;
-    dflash::launch_w4_gemm(dflash::kModeLinear, weight->scale_dtype == DFLASH_DTYPE_F32, p, st);
+    const int mt = token_tiles(m);
+    p.rows_per_pass = 16 * mt;
+    launch_w4(dflash::kModeLinear, weight->scale_dtype == DFLASH_DTYPE_F32, mt, 1, p, st);
     return launch_status("qlinear");
   } catch (...) {
     return fail(DFLASH_ERR_HIP, "unexpected host exception");
@@ -279,9 +342,15 @@ int dflash_router_logits(const void* hidden, int64_t tokens, int64_t hidden_size
     if (tokens == 0) return DFLASH_OK;
     if (!hidden || !router_weight || !logits || !aligned16(hidden) || !aligned16(router_weight))
       return fail(DFLASH_ERR_INVALID_ARGUMENT, "router: NULL or misaligned pointer");
-    dflash::launch_router(static_cast<const uint16_t*>(hidden), static_cast<const uint16_t*>(router_weight), logits,
-                          static_cast<int>(tokens), static_cast<int>(experts), static_cast<int>(hidden_size),
-                          static_cast<hipStream_t>(stream));
+    dflash::FrontParams f{};
+    f.x = static_cast<const uint16_t*>(hidden);
+    f.router_w = static_cast<const uint16_t*>(router_weight);
+    f.logits = logits;
+    f.T = static_cast<int>(tokens);
+    f.E = static_cast<int>(experts);
+    f.H = static_cast<int>(hidden_size);
+    f.n_router = static_cast<int>(((tokens + 15) / 16) * ((experts + 15) / 16));
+    dflash::launch_front(f, static_cast<hipStream_t>(stream));
     return launch_status("router");
   } catch (...) {
     return fail(DFLASH_ERR_HIP, "unexpected host exception");
@@ -289,9 +358,8 @@ int dflash_router_logits(const void* hidden, int64_t tokens, int64_t hidden_size
 }
 
 size_t dflash_moe_route_workspace_bytes(int64_t tokens, int64_t experts, int64_t top_k) {
-  (void)top_k;
-  if (tokens < 0 || experts <= 0) return 0;
-  return route_layout(tokens, experts).total;
+  if (tokens < 0 || experts <= 0 || top_k <= 0) return 0;
+  return route_layout(tokens, top_k, experts).total;
 }
 
 int dflash_moe_route(const float* logits, int64_t tokens, int64_t experts, int64_t top_k, int32_t* topk_ids,
@@ -302,13 +370,12 @@ int dflash_moe_route(const float* logits, int64_t tokens, int64_t experts, int64
     if (!expert_offsets) return fail(DFLASH_ERR_INVALID_ARGUMENT, "expert_offsets is required");
     if (tokens > 0 && (!logits || !topk_ids || !topk_weights || !perm || !inv_perm))
       return fail(DFLASH_ERR_INVALID_ARGUMENT, "route: NULL pointer");
-    const RouteLayout L = route_layout(tokens, experts);
+    const RouteLayout L = route_layout(tokens, top_k, experts);
     if (!workspace || workspace_bytes < L.total || !aligned16(workspace))
       return fail(DFLASH_ERR_WORKSPACE, "route workspace needs " + std::to_string(L.total) + " bytes");
-    dflash::launch_route(logits, static_cast<int>(tokens), static_cast<int>(experts), static_cast<int>(top_k), topk_ids,
-                         topk_weights, perm, inv_perm, expert_offsets, at<int32_t>(workspace, L.hit),
-                         at<int32_t>(workspace, L.meta), at<int32_t>(workspace, L.counts),
-                         at<uint32_t>(workspace, L.bitmap), true, static_cast<hipStream_t>(stream));
+    const dflash::RouteParams r = route_params(logits, tokens, experts, top_k, topk_ids, topk_weights, perm, inv_perm,
+                                               expert_offsets, workspace, L, 16 * token_tiles(tokens), false);
+    dflash::launch_route(r, false, static_cast<hipStream_t>(stream));
     return launch_status("route");
   } catch (...) {
     return fail(DFLASH_ERR_HIP, "unexpected host exception");
@@ -318,7 +385,7 @@ int dflash_moe_route(const float* logits, int64_t tokens, int64_t experts, int64
 size_t dflash_moe_workspace_bytes(int64_t tokens, int64_t hidden_size, int64_t inter_size, int64_t experts,
                                   int64_t top_k, int64_t group_size, int has_shared) {
   if (tokens < 0 || hidden_size <= 0 || inter_size <= 0 || experts <= 0 || top_k <= 0 || group_size <= 0) return 0;
-  return moe_layout(tokens, hidden_size, inter_size, experts, top_k, group_size, has_shared != 0).total;
+  return moe_layout(tokens, hidden_size, inter_size, experts, top_k, has_shared != 0).total;
 }
 
 int dflash_moe_experts_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, int64_t top_k,
@@ -335,16 +402,32 @@ int dflash_moe_experts_w4a16(const void* hidden, int64_t tokens, int64_t hidden_
     if (tokens == 0) return DFLASH_OK;
     if (!topk_weights || !perm || !inv_perm || !expert_offsets)
       return fail(DFLASH_ERR_INVALID_ARGUMENT, "experts: routing arrays are required");
-    const MoeLayout L = moe_layout(S.T, S.H, S.I, S.E, S.k, S.G, S.shared);
+    const MoeLayout L = moe_layout(S.T, S.H, S.I, S.E, S.k, S.shared);
     if (!workspace || workspace_bytes < L.total || !aligned16(workspace))
       return fail(DFLASH_ERR_WORKSPACE, "moe workspace needs " + std::to_string(L.total) + " bytes");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    int32_t* hit = at<int32_t>(workspace, L.route.hit);
-    int32_t* meta = at<int32_t>(workspace, L.route.meta);
-    dflash::launch_hitlist(expert_offsets, static_cast<int>(S.E), hit, meta, st);
-    if (int r = launch_status("hitlist")) return r;
-    return run_experts(S, hidden, topk_weights, perm, inv_perm, expert_offsets, hit, meta, gate_up, down,
-                       shared_gate_up, shared_down, shared_gate_weight, out, workspace, L, st);
+    dflash::TableParams t{};
+    t.offsets = expert_offsets;
+    t.E = static_cast<int>(S.E);
+    t.T = static_cast<int>(S.T);
+    t.hit = at<int32_t>(workspace, L.route.hit);
+    t.pass_start = at<int32_t>(workspace, L.route.pass_start);
+    t.meta = at<int32_t>(workspace, L.route.meta);
+    t.slot_table = at<int4>(workspace, L.route.slot_table);
+    t.pass_slot = at<int32_t>(workspace, L.route.pass_slot);
+    t.rows_per_pass = 16 * token_tiles(S.T);
+    t.has_shared = S.shared ? 1 : 0;
+    t.x = static_cast<const uint16_t*>(hidden);
+    t.H = static_cast<int>(S.H);
+    t.x_il = at<uint16_t>(workspace, L.x_il);
+    t.xneg = at<float>(workspace, L.xneg);
+    t.gate_w = S.shared ? static_cast<const uint16_t*>(shared_gate_weight) : nullptr;
+    t.gate_out = at<float>(workspace, L.gate);
+    dflash::launch_table_prep(t, st);
+    if (int r = launch_status("table_prep")) return r;
+    return run_experts(S, topk_weights, perm, inv_perm, expert_offsets, t.hit, t.pass_start, t.meta, t.slot_table,
+                       t.pass_slot, gate_up, down,
+                       shared_gate_up, shared_down, out, workspace, L, st);
   } catch (...) {
     return fail(DFLASH_ERR_HIP, "unexpected host exception");
   }
@@ -368,29 +451,42 @@ int dflash_moe_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, co
     if (!expert_offsets) return fail(DFLASH_ERR_INVALID_ARGUMENT, "expert_offsets is required");
     if (tokens > 0 && (!topk_ids || !topk_weights || !perm || !inv_perm))
       return fail(DFLASH_ERR_INVALID_ARGUMENT, "routing output arrays are required");
-    const MoeLayout L = moe_layout(S.T, S.H, S.I, S.E, S.k, S.G, S.shared);
+    const MoeLayout L = moe_layout(S.T, S.H, S.I, S.E, S.k, S.shared);
     if (!workspace || workspace_bytes < L.total || !aligned16(workspace))
       return fail(DFLASH_ERR_WORKSPACE, "moe workspace needs " + std::to_string(L.total) + " bytes");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const float* logits = router_logits;
-    if (!logits) {
-      float* dst = logits_out ? logits_out : at<float>(workspace, L.logits);
-      if (tokens > 0) {
-        dflash::launch_router(static_cast<const uint16_t*>(hidden), static_cast<const uint16_t*>(router_weight), dst,
-                              static_cast<int>(S.T), static_cast<int>(S.E), static_cast<int>(S.H), st);
-        if (int r = launch_status("router")) return r;
-      }
-      logits = dst;
+    const int T = static_cast<int>(S.T), E = static_cast<int>(S.E);
+    const bool small = dflash::route_small_fits(T, E, static_cast<int>(S.k));
+    float* logits = router_logits ? const_cast<float*>(router_logits)
+                                  : (logits_out ? logits_out : at<float>(workspace, L.logits));
+    dflash::FrontParams f{};
+    f.x = static_cast<const uint16_t*>(hidden);
+    f.router_w = static_cast<const uint16_t*>(router_weight);
+    f.logits = logits;
+    f.T = T;
+    f.E = E;
+    f.H = static_cast<int>(S.H);
+    f.n_router = router_logits ? 0 : ((T + 15) / 16) * ((E + 15) / 16);
+    f.prep_rows = T;
+    f.x_il = at<uint16_t>(workspace, L.x_il);
+    f.xneg = at<float>(workspace, L.xneg);
+    f.gate_w = S.shared ? static_cast<const uint16_t*>(shared_gate_weight) : nullptr;
+    f.gate_out = at<float>(workspace, L.gate);
+    if (!small) {
+      f.zero = at<uint32_t>(workspace, L.route.counts);
+      f.zero_words = dflash::route_zero_words(T, E);
+      f.n_zero = static_cast<int>(std::min<int64_t>(256, (f.zero_words + 2047) / 2048));
     }
-    int32_t* hit = at<int32_t>(workspace, L.route.hit);
-    int32_t* meta = at<int32_t>(workspace, L.route.meta);
-    dflash::launch_route(logits, static_cast<int>(S.T), static_cast<int>(S.E), static_cast<int>(S.k), topk_ids,
-                         topk_weights, perm, inv_perm, expert_offsets, hit, meta,
-                         at<int32_t>(workspace, L.route.counts), at<uint32_t>(workspace, L.route.bitmap), true, st);
-    if (int r = launch_status("route")) return r;
+    dflash::launch_front(f, st);
+    if (int r = launch_status("front")) return r;
+    const dflash::RouteParams r = route_params(logits, S.T, S.E, S.k, topk_ids, topk_weights, perm, inv_perm,
+                                               expert_offsets, workspace, L.route, 16 * token_tiles(S.T), S.shared);
+    dflash::launch_route(r, true, st);
+    if (int rc = launch_status("route")) return rc;
     if (tokens == 0) return DFLASH_OK;
-    return run_experts(S, hidden, topk_weights, perm, inv_perm, expert_offsets, hit, meta, gate_up, down,
-                       shared_gate_up, shared_down, shared_gate_weight, out, workspace, L, st);
+    return run_experts(S, topk_weights, perm, inv_perm, expert_offsets, r.hit, r.pass_start, r.meta, r.slot_table,
+                       r.pass_slot, gate_up, down,
+                       shared_gate_up, shared_down, out, workspace, L, st);
   } catch (...) {
     return fail(DFLASH_ERR_HIP, "unexpected host exception");
   }

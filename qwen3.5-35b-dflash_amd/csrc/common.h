@@ -29,6 +29,30 @@ constexpr float kDequantOffset = 136.0f;       // 128 + 8 (sign flip of the nibb
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt untouched).  Used right after loads
+// issued under a condition inside a loop, so later uses of those registers
+// need no conservative full wait on every iteration.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Load of a wave-uniform element through the constant address space: with a
+// readfirstlane'd index it becomes s_load (counted by lgkmcnt), so it never
+// waits behind the vector loads a wave keeps in flight.  Only for memory the
+// running kernel does not write.
+template <typename T>
+__device__ __forceinline__ T ld_const(const T* p, int i) {
+  i = __builtin_amdgcn_readfirstlane(i);
+  return ((const __attribute__((address_space(4))) T*)(p))[i];  // address-space cast
+}
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte wave-uniform record as one s_load_dwordx4.
+__device__ __forceinline__ int4 ld_const_int4(const int4* p, int i) {
+  i = __builtin_amdgcn_readfirstlane(i);
+  const i32x4 v = ((const __attribute__((address_space(4))) i32x4*)(p))[i];
+  return make_int4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bits) {
   uint32_t d;
   // gfx9 VOP3 reads at most one SGPR: mask from an SGPR, the magic bits from a VGPR.
@@ -69,6 +93,15 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
+// Raw scale bits (no conversion at load time, so a prefetched scale does not
+// force a wait on the loads issued before it) and their fp32 value.
+__device__ __forceinline__ uint32_t load_scale_bits(const uint16_t* p) { return *p; }
+__device__ __forceinline__ uint32_t load_scale_bits(const float* p) { return __float_as_uint(*p); }
+template <typename ScaleT>
+__device__ __forceinline__ float scale_value(uint32_t bits) {
+  return sizeof(ScaleT) == 2 ? __uint_as_float(bits << 16) : __uint_as_float(bits);
+}
+
 template <typename ScaleT>
 __device__ __forceinline__ float load_scale(const ScaleT* p);
 template <>
@@ -79,12 +112,16 @@ __device__ __forceinline__ float load_scale<float>(const float* p) { return *p; 
 // Interleaved position of column c inside its octet (k0 k4 k1 k5 k2 k6 k3 k7).
 __device__ __forceinline__ int octet_slot(int c) { return (c & ~7) | ((c & 3) << 1) | ((c >> 2) & 1); }
 
-// Sum over the 16 lanes that share (lane >> 4).
+// Sum over the 16 lanes that share (lane >> 4): DPP row rotations, no LDS trip.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
+}
 __device__ __forceinline__ float row16_sum(float v) {
-  v += __shfl_xor(v, 1, 64);
-  v += __shfl_xor(v, 2, 64);
-  v += __shfl_xor(v, 4, 64);
-  v += __shfl_xor(v, 8, 64);
+  v += dpp_f32<0x121>(v);  // row_ror:1
+  v += dpp_f32<0x122>(v);  // row_ror:2
+  v += dpp_f32<0x124>(v);  // row_ror:4
+  v += dpp_f32<0x128>(v);  // row_ror:8
   return v;
 }
 

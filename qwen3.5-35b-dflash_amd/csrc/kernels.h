@@ -5,35 +5,106 @@
 
 namespace dflash {
 
-// Single-workgroup routing limits (LDS-resident ids and membership bitmap).
-constexpr int kSmallPairs = 2048;        // T * k
-constexpr int kSmallBitmapWords = 8192;  // T * ceil(E / 32)
 constexpr int kMaxExperts = 1024;
 constexpr int kMaxTopK = 64;
+// Single-workgroup routing limits (LDS-resident slot map).
+constexpr int kSmallPairs = 2048;       // T * k
+constexpr int kSmallSlotBytes = 32768;  // roundup(T, 4) * E
+
+__device__ __forceinline__ int wave_sum_int(int v) {
+  for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Router tiles + activation prep + zeroing, in one launch (front_kernel).
+struct FrontParams {
+  const uint16_t* x;        // bf16 [T][H]
+  const uint16_t* router_w; // bf16 [E][H]
+  float* logits;            // fp32 [T][E]
+  int T, E, H;
+  int n_router;             // router tiles (0 when the logits are given)
+  int prep_rows;            // rows of x to prepare (T, or 0 for router tiles only)
+  uint16_t* x_il;           // octet-interleaved copy of x [T][H]
+  float* xneg;              // -136 * sum per 128-column block [T][H/128]
+  const uint16_t* gate_w;   // shared-expert gate vector [H] or null
+  float* gate_out;          // sigmoid gate [T]
+  uint32_t* zero;           // words cleared by the launch
+  int64_t zero_words;
+  int n_zero;               // blocks assigned to clearing
+};
+
+struct RouteParams {
+  const float* logits;  // [T][E]
+  int T, E, k;
+  int32_t* ids;         // [T][k]
+  float* wts;           // [T][k]
+  int32_t* perm;        // [T*k]
+  int32_t* inv;         // [T*k]
+  int32_t* offsets;     // [E+1]
+  int32_t* hit;         // [E] hit experts, ascending
+  int32_t* pass_start;  // [E+2] first pass of each slot, then the total
+  int32_t* meta;        // [0] hit experts, [1] total passes
+  int32_t* counts;      // [E], followed in memory by the slot map (multi-workgroup path)
+  uint8_t* slotmap;     // [E][T]
+  int4* slot_table;     // [E+1] per slot: expert (-1 shared), segment start, rows, first pass
+  int32_t* pass_slot;   // [T*k + T] slot of every pass
+  int rows_per_pass;
+  int has_shared;
+};
+
+struct TableParams {
+  const int32_t* offsets;
+  int E, T;
+  int32_t* hit;
+  int32_t* pass_start;
+  int32_t* meta;
+  int4* slot_table;
+  int32_t* pass_slot;
+  int rows_per_pass, has_shared;
+  // prep
+  const uint16_t* x;
+  int H;
+  uint16_t* x_il;
+  float* xneg;
+  const uint16_t* gate_w;
+  float* gate_out;
+};
+
+// Record slot `slot` (expert e, or -1 for the shared expert) in the work table.
+__device__ __forceinline__ void write_slot(int4* slot_table, int32_t* pass_slot, int slot, int e, int seg, int rows,
+                                           int pass0, int rows_per_pass) {
+  slot_table[slot] = make_int4(e, seg, rows, pass0);
+  const int n = (rows + rows_per_pass - 1) / rows_per_pass;
+  for (int i = 0; i < n; ++i) pass_slot[pass0 + i] = slot;
+}
 
 enum W4Mode : int { kModeLinear = 0, kModeGateUp = 1, kModeDown = 2 };
 
-// One launch of the small-M grouped W4A16 GEMM.  A "slot" is a hit expert
-// (or the shared expert, which follows the hit experts); a work item is one
-// wave computing a 32-row strip of the slot's weight matrix for all of the
-// slot's tokens.
-struct W4GemmParams {
+// Persistent streaming W4A16 GEMM over the routing work table (w4_stream.hip).
+struct W4StreamParams {
   const uint8_t* w;        // packed int4 [E][N][K/2] (or [N][K/2] for kModeLinear)
   const void* s;           // scales [E][N][K/G], bf16 or fp32
   const uint8_t* w_shared; // shared-expert packed [N][K/2] or null
-  const void* s_shared;    // shared-expert scales [N][K/G]
+  const void* s_shared;
   int64_t w_stride;        // bytes per expert
   int64_t s_stride;        // scale elements per expert
   int N, K, G;
-  // activations: octet-interleaved bf16 rows of length K, and -136*sum terms
+  // activations: octet-interleaved bf16 rows of length K and their -136*sum
+  // per 128-column block, given as neg_parts consecutive partial sums
   const uint16_t* act;
-  const float* act_neg;    // [rows][K/G] (kNegParts == 1) or [rows][K/16] partials
-  // routing
-  const int32_t* perm;     // sorted position -> flat pair t*k+slot
-  const int32_t* offsets;  // [E+1]
-  const int32_t* hit;      // hit experts, ascending
-  const int32_t* meta;     // meta[0] = number of hit experts
+  const float* act_neg;
+  int neg_parts;
+  // work table
+  const int32_t* perm;
+  const int32_t* offsets;
+  const int32_t* hit;
+  const int32_t* pass_start;
+  const int32_t* meta;
+  const int4* slot_table;  // per slot: expert (-1 shared), segment start, rows, first pass
+  const int32_t* pass_slot;
   int top_k, T, has_shared;
+  int rows_per_pass;       // 16 * MT
+  int strips;              // units per pass
   // outputs
   uint16_t* out_bf16;      // kModeLinear: [M][N]; kModeGateUp: h [(T*k+T)][N/2] interleaved
   float* out_part;         // kModeGateUp: [(T*k+T)][N/32] partial -136*sum(h) per 16 columns
@@ -41,20 +112,22 @@ struct W4GemmParams {
   const float* route_w;    // kModeDown: flat routing weights [T*k]
   const float* shared_gate;// kModeDown: sigmoid gate [T]
   int M;                   // kModeLinear rows
-  int items_per_slot;
-  int max_slots;
 };
 
-void launch_prep(const uint16_t* x, int rows, int K, int group, uint16_t* x_il, float* xneg, const uint16_t* gate_w,
-                 float* gate_out, hipStream_t stream);
-void launch_router(const uint16_t* x, const uint16_t* w, float* logits, int T, int E, int H, hipStream_t stream);
+void launch_front(const FrontParams& p, hipStream_t stream);
 bool route_small_fits(int T, int E, int k);
-void launch_route(const float* logits, int T, int E, int k, int32_t* ids, float* wts, int32_t* perm, int32_t* inv,
-                  int32_t* offsets, int32_t* hit, int32_t* meta, int32_t* counts, uint32_t* bitmap, bool allow_small,
-                  hipStream_t stream);
-void launch_hitlist(const int32_t* offsets, int E, int32_t* hit, int32_t* meta, hipStream_t stream);
+int64_t route_zero_words(int T, int E);
+void launch_route(const RouteParams& p, bool zeroed, hipStream_t stream);
+void launch_table_prep(const TableParams& p, hipStream_t stream);
 void launch_combine(const float* y, const int32_t* inv, int T, int k, int H, int has_shared, uint16_t* out,
                     hipStream_t stream);
-void launch_w4_gemm(int mode, bool fp32_scales, const W4GemmParams& p, hipStream_t stream);
+// Per-wave fallback for any K % 512 == 0 (w4_gemm.hip); max_slots bounds the hit experts + shared.
+void launch_w4_gemm(int mode, bool fp32_scales, int max_slots, const W4StreamParams& p, hipStream_t stream);
+// K in {512, 1024, 2048} and group 128 (spill-free register budgets); K = 512 splits 4 ways with 2 row groups,
+// larger K 8 ways with 1.
+bool w4_stream_supports(int K, int G);
+int w4_stream_row_groups(int K);
+// mt: token tiles per pass (1 or 2); grid: persistent workgroups (one per CU)
+void launch_w4_stream(int mode, bool fp32_scales, int mt, int grid, const W4StreamParams& p, hipStream_t stream);
 
 }  // namespace dflash

@@ -1,5 +1,5 @@
-// Router logits, top-k routing with renormalised weights, the stable
-// token-to-expert permutation, activation preparation and the final combine.
+// Router logits, activation preparation, top-k routing with renormalised
+// weights, the stable token-to-expert permutation, and the final combine.
 //
 // Routing contract (reference reference/fused_ops.py:160-164,
 // graph/fused/quant_target.py:168-172): rank the fp32 logits in descending
@@ -9,89 +9,167 @@
 // docs/reference/qwen35-moe-operators-and-quantization-analysis.md:685-707):
 // flat pairs t*k+slot sorted by expert, stable, so a segment lists its tokens
 // in ascending order.
+//
+// Besides the reference outputs the routing kernels emit the work table the
+// expert GEMMs consume: the hit experts in ascending order (then the shared
+// expert as one more slot) and, per slot, the first "pass" index, a pass being
+// up to rows_per_pass of the slot's tokens.
+#include <algorithm>
+
 #include "kernels.h"
 
 namespace dflash {
 
 // ---------------------------------------------------------------------------
-// Activation preparation: octet-interleaved copy of x, -136*sum per group and
-// (optionally) the shared-expert gate sigmoid(x . w_gate).
-// grid = rows, block = 256.  Requires K % 8 == 0 and group % 8 == 0, group <= 512.
-__global__ __launch_bounds__(256) void prep_kernel(const uint16_t* __restrict__ x, int K, int group,
-                                                   uint16_t* __restrict__ x_il, float* __restrict__ xneg,
-                                                   const uint16_t* __restrict__ gate_w,
-                                                   float* __restrict__ gate_out) {
-  const int row = blockIdx.x;
-  const uint4* src = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(row) * K);
-  uint4* dst = reinterpret_cast<uint4*>(x_il + static_cast<int64_t>(row) * K);
-  const int chunks = K >> 3;
-  const int per_group = group >> 3;
-  float gate_acc = 0.f;
-  for (int base = 0; base < chunks; base += 256) {
-    const int c = base + threadIdx.x;
-    float sum = 0.f;
-    if (c < chunks) {
-      const uint4 v = src[c];
-      // natural pairs (0,1)(2,3)(4,5)(6,7) -> (0,4)(1,5)(2,6)(3,7)
-      uint4 o;
-      o.x = (v.x & 0xFFFFu) | (v.z << 16);
-      o.y = (v.x >> 16) | (v.z & 0xFFFF0000u);
-      o.z = (v.y & 0xFFFFu) | (v.w << 16);
-      o.w = (v.y >> 16) | (v.w & 0xFFFF0000u);
-      dst[c] = o;
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-      float gw[8];
-      if (gate_w) {
-        const uint4 g = reinterpret_cast<const uint4*>(gate_w)[c];
-        const uint32_t gg[4] = {g.x, g.y, g.z, g.w};
+// DPP helpers (64-bit max over a wave without LDS round trips).
+template <int kCtrl>
+__device__ __forceinline__ uint64_t dpp64(uint64_t v) {
+  const uint32_t lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(v), kCtrl, 0xF, 0xF, false);
+  const uint32_t hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(v >> 32), kCtrl, 0xF, 0xF, false);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int lane) {
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(v), lane);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(v >> 32), lane);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// Max over all 64 lanes, returned wave-uniform.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  v = umax64(v, dpp64<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = umax64(v, dpp64<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = umax64(v, dpp64<0x141>(v));  // row_half_mirror
+  v = umax64(v, dpp64<0x140>(v));  // row_mirror: every lane of a 16-lane row holds the row max
+  return umax64(umax64(readlane64(v, 0), readlane64(v, 16)), umax64(readlane64(v, 32), readlane64(v, 48)));
+}
+
+// Order-preserving uint32 of a float: -0 folded to +0, NaN ranks below -inf.
+__device__ __forceinline__ uint32_t sortable_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0u;
+  if ((u & 0x7FFFFFFFu) == 0u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float key_to_float(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+// Top-k of one token's logits by one wave: k rounds of a wave-wide 64-bit max
+// over (key << 32 | ~id), so the larger logit wins and, among equal logits,
+// the lower expert id.  Lane s < k ends with (id_s, weight_s).
+template <int kPer>
+__device__ __forceinline__ void wave_topk(const float* __restrict__ row, int E, int k, int* id_out, float* w_out) {
+  const int lane = lane_id();
+  uint64_t key[kPer];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          gw[2 * i] = __uint_as_float(gg[i] << 16);
-          gw[2 * i + 1] = __uint_as_float(gg[i] & 0xFFFF0000u);
-        }
-      }
+  for (int i = 0; i < kPer; ++i) {
+    const int e = lane + 64 * i;
+    key[i] = (e < E) ? ((static_cast<uint64_t>(sortable_key(row[e])) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(e)))
+                     : 0ull;
+  }
+  int my_id = -1;
+  uint32_t my_key = 0;
+  for (int s = 0; s < k; ++s) {
+    uint64_t best = key[0];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float lo = __uint_as_float(w[i] << 16), hi = __uint_as_float(w[i] & 0xFFFF0000u);
-        sum += lo + hi;
-        if (gate_w) gate_acc += lo * gw[2 * i] + hi * gw[2 * i + 1];
-      }
-    }
-    // group sums: per_group consecutive chunks sit in consecutive lanes of one wave
-    for (int o = 1; o < per_group; o <<= 1) sum += __shfl_xor(sum, o, 64);
-    if (c < chunks && (c % per_group) == 0) xneg[static_cast<int64_t>(row) * (K / group) + c / per_group] = -kDequantOffset * sum;
-  }
-  if (gate_w) {
-    __shared__ float part[4];
-    gate_acc = wave_sum(gate_acc);
-    if (lane_id() == 0) part[threadIdx.x >> 6] = gate_acc;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const float z = part[0] + part[1] + part[2] + part[3];
-      gate_out[row] = 1.0f / (1.0f + __expf(-z));
+    for (int i = 1; i < kPer; ++i) best = umax64(best, key[i]);
+    best = wave_max_u64(best);
+    const int e = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(best));
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+      if (lane + 64 * i == e) key[i] = 0ull;
+    if (lane == s) {
+      my_id = e;
+      my_key = static_cast<uint32_t>(best >> 32);
     }
   }
+  const float top = key_to_float(__builtin_amdgcn_readlane(static_cast<int>(my_key), 0));
+  const float ex = (lane < k) ? expf(key_to_float(my_key) - top) : 0.f;
+  const float total = wave_sum(ex);
+  *id_out = my_id;
+  *w_out = ex / total;
+}
+
+__device__ __forceinline__ void topk_any(const float* row, int E, int k, int* id, float* w) {
+  if (E <= 64) wave_topk<1>(row, E, k, id, w);
+  else if (E <= 128) wave_topk<2>(row, E, k, id, w);
+  else if (E <= 256) wave_topk<4>(row, E, k, id, w);
+  else if (E <= 512) wave_topk<8>(row, E, k, id, w);
+  else wave_topk<16>(row, E, k, id, w);
+}
+
+__device__ __forceinline__ int passes_for(int rows, int rows_per_pass) {
+  return (rows + rows_per_pass - 1) / rows_per_pass;
 }
 
 // ---------------------------------------------------------------------------
-// Router logits fp32 [T][E] = x bf16 [T][H] . W bf16 [E][H]^T on MFMA.
-// grid = (ceil(T/16), ceil(E/16)), block = 512 (8 waves split H; H % 256 == 0).
-__global__ __launch_bounds__(512) void router_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-                                                     float* __restrict__ logits, int T, int E, int H) {
+// Activation preparation of one row of x: octet-interleaved copy, the
+// -136*sum per 128-column block, and (optionally) sigmoid(x . gate_w).
+// Executed by the first 256 threads of a block.  K % 128 == 0.
+__device__ __forceinline__ void prep_row(const uint16_t* __restrict__ x, int K, int row, uint16_t* __restrict__ x_il,
+                                         float* __restrict__ xneg, const uint16_t* __restrict__ gate_w,
+                                         float* __restrict__ gate_out) {
+  __shared__ float part[4];
+  const int tid = threadIdx.x;
+  const uint4* src = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(row) * K);
+  uint4* dst = reinterpret_cast<uint4*>(x_il + static_cast<int64_t>(row) * K);
+  const int chunks = K >> 3;
+  float gate_acc = 0.f;
+  if (tid < 256) {
+    for (int base = 0; base < chunks; base += 256) {
+      const int c = base + tid;
+      float sum = 0.f;
+      if (c < chunks) {
+        const uint4 v = src[c];
+        uint4 o;  // natural pairs (0,1)(2,3)(4,5)(6,7) -> (0,4)(1,5)(2,6)(3,7)
+        o.x = (v.x & 0xFFFFu) | (v.z << 16);
+        o.y = (v.x >> 16) | (v.z & 0xFFFF0000u);
+        o.z = (v.y & 0xFFFFu) | (v.w << 16);
+        o.w = (v.y >> 16) | (v.w & 0xFFFF0000u);
+        dst[c] = o;
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        uint32_t gg[4] = {0u, 0u, 0u, 0u};
+        if (gate_w) {
+          const uint4 g = reinterpret_cast<const uint4*>(gate_w)[c];
+          gg[0] = g.x; gg[1] = g.y; gg[2] = g.z; gg[3] = g.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float lo = __uint_as_float(w[i] << 16), hi = __uint_as_float(w[i] & 0xFFFF0000u);
+          sum += lo + hi;
+          gate_acc += lo * __uint_as_float(gg[i] << 16) + hi * __uint_as_float(gg[i] & 0xFFFF0000u);
+        }
+      }
+      sum = row16_sum(sum);  // 16 chunks of 8 = one 128-column block, in 16 consecutive lanes
+      if (c < chunks && (c & 15) == 0) xneg[static_cast<int64_t>(row) * (K >> 7) + (c >> 4)] = -kDequantOffset * sum;
+    }
+  }
+  if (gate_w) {
+    gate_acc = wave_sum(gate_acc);
+    if (lane_id() == 0 && tid < 256) part[tid >> 6] = gate_acc;
+    __syncthreads();
+    if (tid == 0) gate_out[row] = 1.0f / (1.0f + __expf(-(part[0] + part[1] + part[2] + part[3])));
+  }
+}
+
+// Router logits for a 16x16 tile: fp32 [T][E] = x bf16 [T][H] . W bf16 [E][H]^T;
+// 8 waves split H (H % 256 == 0) and are reduced through LDS.
+__device__ __forceinline__ void router_tile(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                            float* __restrict__ logits, int T, int E, int H, int t0, int e0) {
   __shared__ f32x4 red[8][64];
   const int wave = threadIdx.x >> 6, lane = lane_id();
   const int lr = lane & 15, kq = lane >> 4;
-  const int t0 = blockIdx.x * 16, e0 = blockIdx.y * 16;
   const int trow = min(t0 + lr, T - 1), erow = min(e0 + lr, E - 1);
   const int span = H >> 3;
   const uint16_t* xa = x + static_cast<int64_t>(trow) * H + wave * span + kq * 8;
   const uint16_t* wb = w + static_cast<int64_t>(erow) * H + wave * span + kq * 8;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int k = 0; k < span; k += 32) {
-    const uint4 a = *reinterpret_cast<const uint4*>(xa + k);
-    const uint4 b = *reinterpret_cast<const uint4*>(wb + k);
-    acc = mfma16x16x32(a, b, acc);
-  }
+  for (int k = 0; k < span; k += 32)
+    acc = mfma16x16x32(*reinterpret_cast<const uint4*>(xa + k), *reinterpret_cast<const uint4*>(wb + k), acc);
   red[wave][lane] = acc;
   __syncthreads();
   if (wave == 0) {
@@ -107,251 +185,257 @@ __global__ __launch_bounds__(512) void router_kernel(const uint16_t* __restrict_
   }
 }
 
-// ---------------------------------------------------------------------------
-// Top-k of one token's logits by one wave.  Lane s < k ends with (id, weight).
-// Keys: order-preserving uint32 of the float (-0 folded to +0, NaN lowest),
-// packed with ~id so one 64-bit max picks the larger logit, then the lower id.
-__device__ __forceinline__ uint32_t sortable_key(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0u;  // NaN ranks last
-  if ((u & 0x7FFFFFFFu) == 0u) u = 0u;             // -0 == +0
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-__device__ __forceinline__ float key_to_float(uint32_t k) {
-  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
-}
-
-template <int kPer>
-__device__ __forceinline__ void wave_topk(const float* __restrict__ row, int E, int k, int* id_out,
-                                          float* w_out) {
-  const int lane = lane_id();
-  uint64_t key[kPer];
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int e = lane + 64 * i;
-    key[i] = (e < E) ? ((static_cast<uint64_t>(sortable_key(row[e])) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(e)))
-                     : 0ull;
+// One launch doing the work that needs no routing: router tiles (optional),
+// activation prep rows, and zeroing of the multi-workgroup routing buffers.
+// block = 512.  blocks: [0, n_router) router tiles, then prep_rows prep rows,
+// then n_zero blocks clearing zero_words 32-bit words.
+__global__ __launch_bounds__(512) void front_kernel(FrontParams p) {
+  int b = blockIdx.x;
+  if (b < p.n_router) {
+    const int tiles_e = (p.E + 15) / 16;
+    router_tile(p.x, p.router_w, p.logits, p.T, p.E, p.H, (b / tiles_e) * 16, (b % tiles_e) * 16);
+    return;
   }
-  int my_id = -1;
-  uint32_t my_key = 0;
-  for (int s = 0; s < k; ++s) {
-    uint64_t best = 0;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) best = key[i] > best ? key[i] : best;
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint64_t other = __shfl_xor(best, o, 64);
-      best = other > best ? other : best;
-    }
-    const int e = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(best));
-    if ((e & 63) == lane) {
-#pragma unroll
-      for (int i = 0; i < kPer; ++i)
-        if (lane + 64 * i == e) key[i] = 0ull;
-    }
-    if (lane == s) {
-      my_id = e;
-      my_key = static_cast<uint32_t>(best >> 32);
-    }
+  b -= p.n_router;
+  if (b < p.prep_rows) {
+    prep_row(p.x, p.H, b, p.x_il, p.xneg, p.gate_w, p.gate_out);
+    return;
   }
-  const float top = key_to_float(__shfl(my_key, 0, 64));
-  const float ex = (lane < k) ? expf(key_to_float(my_key) - top) : 0.f;
-  const float total = wave_sum(ex);
-  *id_out = my_id;
-  *w_out = ex / total;
-}
-
-__device__ __forceinline__ void topk_any(const float* row, int E, int k, int* id, float* w) {
-  if (E <= 64) wave_topk<1>(row, E, k, id, w);
-  else if (E <= 128) wave_topk<2>(row, E, k, id, w);
-  else if (E <= 256) wave_topk<4>(row, E, k, id, w);
-  else if (E <= 512) wave_topk<8>(row, E, k, id, w);
-  else wave_topk<16>(row, E, k, id, w);
+  b -= p.prep_rows;
+  for (int64_t i = static_cast<int64_t>(b) * 512 + threadIdx.x; i < p.zero_words;
+       i += static_cast<int64_t>(p.n_zero) * 512)
+    p.zero[i] = 0u;
 }
 
 // ---------------------------------------------------------------------------
-// Single-workgroup routing for small T: top-k, counts, offsets, hit list and
-// the stable permutation without leaving the workgroup.
-// block = 1024; T*k <= kSmallPairs, E <= 1024, k <= 64.
-__global__ __launch_bounds__(1024) void route_small_kernel(const float* __restrict__ logits, int T, int E, int k,
-                                                           int32_t* __restrict__ ids, float* __restrict__ wts,
-                                                           int32_t* __restrict__ perm, int32_t* __restrict__ inv,
-                                                           int32_t* __restrict__ offsets, int32_t* __restrict__ hit,
-                                                           int32_t* __restrict__ meta) {
-  __shared__ int counts[1024];
-  __shared__ int offs[1024];
-  __shared__ int wave_tot[2][16];
-  __shared__ int lds_ids[kSmallPairs];
-  __shared__ uint32_t bits[kSmallBitmapWords];
+// Single-workgroup routing for small T (route_small_fits).
+// LDS slot map [E][tpad]: byte = slot+1 of token t in expert e, or 0.
+__global__ __launch_bounds__(1024) void route_small_kernel(RouteParams p) {
+  __shared__ int counts[kMaxExperts];
+  __shared__ int wave_tot[3][16];
+  __shared__ uint32_t slotmap_words[kSmallSlotBytes / 4];
+  uint8_t* slotmap = reinterpret_cast<uint8_t*>(slotmap_words);
+  const int T = p.T, E = p.E, k = p.k;
   const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id();
-  const int words = (E + 31) >> 5;
-  for (int i = tid; i < 1024; i += 1024) counts[i] = 0;
-  for (int i = tid; i < T * words; i += 1024) bits[i] = 0u;
+  const int tpad = (T + 3) & ~3;
+  for (int i = tid; i < kMaxExperts; i += 1024) counts[i] = 0;
+  for (int i = tid; i < (E * tpad) / 4; i += 1024) slotmap_words[i] = 0u;
   __syncthreads();
   for (int t = wave; t < T; t += 16) {
     int id;
     float w;
-    topk_any(logits + static_cast<int64_t>(t) * E, E, k, &id, &w);
+    topk_any(p.logits + static_cast<int64_t>(t) * E, E, k, &id, &w);
     if (lane < k) {
-      ids[t * k + lane] = id;
-      wts[t * k + lane] = w;
-      lds_ids[t * k + lane] = id;
+      p.ids[t * k + lane] = id;
+      p.wts[t * k + lane] = w;
       atomicAdd(&counts[id], 1);
-      atomicOr(&bits[t * words + (id >> 5)], 1u << (id & 31));
+      slotmap[id * tpad + t] = static_cast<uint8_t>(lane + 1);
     }
   }
   __syncthreads();
-  // exclusive scans over experts: token offsets and hit-list positions
+  // exclusive scans over experts: segment offsets, hit index, first pass
   const int cnt = tid < E ? counts[tid] : 0;
-  int incl = cnt, nz = cnt > 0 ? 1 : 0;
+  const int npass = passes_for(cnt, p.rows_per_pass);
+  int a = cnt, b = cnt > 0 ? 1 : 0, c = npass;
   for (int o = 1; o < 64; o <<= 1) {
-    const int a = __shfl_up(incl, o, 64), b = __shfl_up(nz, o, 64);
+    const int ua = __shfl_up(a, o, 64), ub = __shfl_up(b, o, 64), uc = __shfl_up(c, o, 64);
     if (lane >= o) {
-      incl += a;
-      nz += b;
+      a += ua;
+      b += ub;
+      c += uc;
     }
   }
   if (lane == 63) {
-    wave_tot[0][wave] = incl;
-    wave_tot[1][wave] = nz;
+    wave_tot[0][wave] = a;
+    wave_tot[1][wave] = b;
+    wave_tot[2][wave] = c;
   }
   __syncthreads();
-  int base = 0, nzbase = 0;
+  int ba = 0, bb = 0, bc = 0;
   for (int i = 0; i < wave; ++i) {
-    base += wave_tot[0][i];
-    nzbase += wave_tot[1][i];
+    ba += wave_tot[0][i];
+    bb += wave_tot[1][i];
+    bc += wave_tot[2][i];
   }
-  const int excl = base + incl - cnt;
-  const int nzexcl = nzbase + nz - (cnt > 0 ? 1 : 0);
+  const int off = ba + a - cnt, hit_idx = bb + b - (cnt > 0 ? 1 : 0), pass0 = bc + c - npass;
   if (tid < E) {
-    offs[tid] = excl;
-    offsets[tid] = excl;
-    if (cnt > 0) hit[nzexcl] = tid;
+    p.offsets[tid] = off;
+    if (cnt > 0) {
+      p.hit[hit_idx] = tid;
+      p.pass_start[hit_idx] = pass0;
+      write_slot(p.slot_table, p.pass_slot, hit_idx, tid, off, cnt, pass0, p.rows_per_pass);
+    }
     if (tid == E - 1) {
-      offsets[E] = excl + cnt;
-      meta[0] = nzexcl + (cnt > 0 ? 1 : 0);
+      const int nh = hit_idx + (cnt > 0 ? 1 : 0);
+      int total = pass0 + npass;
+      p.offsets[E] = off + cnt;
+      p.pass_start[nh] = total;
+      if (p.has_shared) {
+        write_slot(p.slot_table, p.pass_slot, nh, -1, 0, T, total, p.rows_per_pass);
+        total += passes_for(T, p.rows_per_pass);
+      }
+      p.pass_start[nh + p.has_shared] = total;
+      p.meta[0] = nh;
+      p.meta[1] = total;
     }
   }
-  __syncthreads();
-  // stable ranks: expert tid walks the tokens in ascending order
+  // stable ranks: expert tid walks its slot-map row (tokens ascending)
   if (tid < E && cnt > 0) {
-    int pos = offs[tid];
-    const int wi = tid >> 5;
-    const uint32_t bit = 1u << (tid & 31);
-    for (int t = 0; t < T; ++t) {
-      if (bits[t * words + wi] & bit) {
-        int s = 0;
-        while (s < k && lds_ids[t * k + s] != tid) ++s;
-        if (s < k) {
-          perm[pos] = t * k + s;
-          inv[t * k + s] = pos;
-        }
+    int pos = off;
+    const uint32_t* row = slotmap_words + (tid * tpad) / 4;
+    for (int q = 0; q < tpad / 4; ++q) {
+      uint32_t word = row[q];
+      while (word) {
+        const int byte = __builtin_ctz(word) >> 3;
+        const int flat = (q * 4 + byte) * k + static_cast<int>((word >> (byte * 8)) & 0xFFu) - 1;
+        p.perm[pos] = flat;
+        p.inv[flat] = pos;
         ++pos;
+        word &= ~(0xFFu << (byte * 8));
       }
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Multi-workgroup routing for large T.
-__global__ void route_zero_kernel(int32_t* __restrict__ counts, int E) {
-  for (int i = threadIdx.x; i < E; i += blockDim.x) counts[i] = 0;
+// Multi-workgroup routing for large T.  The counts and the slot map [E][T]
+// (bytes) must be zero on entry: front_kernel or route_zero_kernel clears them.
+__global__ void route_zero_kernel(uint32_t* __restrict__ words, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    words[i] = 0u;
 }
 
 // grid = ceil(T/4), block = 256: one wave per token.
-__global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ logits, int T, int E, int k,
-                                                         int32_t* __restrict__ ids, float* __restrict__ wts,
-                                                         int32_t* __restrict__ counts, uint32_t* __restrict__ bitmap) {
+__global__ __launch_bounds__(256) void route_topk_kernel(RouteParams p) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = lane_id();
-  if (t >= T) return;
+  if (t >= p.T) return;
   int id;
   float w;
-  topk_any(logits + static_cast<int64_t>(t) * E, E, k, &id, &w);
-  if (lane < k) {
-    ids[static_cast<int64_t>(t) * k + lane] = id;
-    wts[static_cast<int64_t>(t) * k + lane] = w;
-    atomicAdd(&counts[id], 1);
+  topk_any(p.logits + static_cast<int64_t>(t) * p.E, p.E, p.k, &id, &w);
+  if (lane < p.k) {
+    p.ids[static_cast<int64_t>(t) * p.k + lane] = id;
+    p.wts[static_cast<int64_t>(t) * p.k + lane] = w;
+    atomicAdd(&p.counts[id], 1);
+    p.slotmap[static_cast<int64_t>(id) * p.T + t] = static_cast<uint8_t>(lane + 1);
   }
-  // E <= 1024 keeps the bitmap row within 32 words: lane w builds word w.
-  const int words = (E + 31) >> 5;
-  uint32_t word = 0;
-  for (int s = 0; s < k; ++s) {
-    const int e = __shfl(id, s, 64);  // uniform loop: every lane takes part
-    if ((e >> 5) == lane) word |= 1u << (e & 31);
-  }
-  if (lane < words) bitmap[static_cast<int64_t>(t) * words + lane] = word;
 }
 
 // grid = ceil(E/4), block = 256: one wave per expert.
-__global__ __launch_bounds__(256) void route_permute_kernel(const int32_t* __restrict__ ids, const int32_t* __restrict__ counts,
-                                                            const uint32_t* __restrict__ bitmap, int T, int E, int k,
-                                                            int32_t* __restrict__ perm, int32_t* __restrict__ inv,
-                                                            int32_t* __restrict__ offsets, int32_t* __restrict__ hit,
-                                                            int32_t* __restrict__ meta) {
+__global__ __launch_bounds__(256) void route_permute_kernel(RouteParams p) {
   const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = lane_id();
-  if (e >= E) return;
-  int before = 0, nz_before = 0;
+  if (e >= p.E) return;
+  int before = 0, nz_before = 0, pass_before = 0;
   for (int i = lane; i < e; i += 64) {
-    const int c = counts[i];
+    const int c = p.counts[i];
     before += c;
     nz_before += c > 0 ? 1 : 0;
+    pass_before += passes_for(c, p.rows_per_pass);
   }
-  for (int o = 1; o < 64; o <<= 1) {
-    before += __shfl_xor(before, o, 64);
-    nz_before += __shfl_xor(nz_before, o, 64);
-  }
-  const int cnt = counts[e];
+  before = wave_sum_int(before);
+  nz_before = wave_sum_int(nz_before);
+  pass_before = wave_sum_int(pass_before);
+  const int cnt = p.counts[e];
   if (lane == 0) {
-    offsets[e] = before;
-    if (cnt > 0) hit[nz_before] = e;
-    if (e == E - 1) {
-      offsets[E] = before + cnt;
-      meta[0] = nz_before + (cnt > 0 ? 1 : 0);
+    p.offsets[e] = before;
+    if (cnt > 0) {
+      p.hit[nz_before] = e;
+      p.pass_start[nz_before] = pass_before;
+      write_slot(p.slot_table, p.pass_slot, nz_before, e, before, cnt, pass_before, p.rows_per_pass);
+    }
+    if (e == p.E - 1) {
+      const int nh = nz_before + (cnt > 0 ? 1 : 0);
+      int total = pass_before + passes_for(cnt, p.rows_per_pass);
+      p.offsets[p.E] = before + cnt;
+      p.pass_start[nh] = total;
+      if (p.has_shared) {
+        write_slot(p.slot_table, p.pass_slot, nh, -1, 0, p.T, total, p.rows_per_pass);
+        total += passes_for(p.T, p.rows_per_pass);
+      }
+      p.pass_start[nh + p.has_shared] = total;
+      p.meta[0] = nh;
+      p.meta[1] = total;
     }
   }
   if (cnt == 0) return;
-  const int words = (E + 31) >> 5;
-  const uint32_t bit = 1u << (e & 31);
+  const uint8_t* row = p.slotmap + static_cast<int64_t>(e) * p.T;
   int running = 0;
-  for (int t0 = 0; t0 < T; t0 += 64) {
+  for (int t0 = 0; t0 < p.T; t0 += 64) {
     const int t = t0 + lane;
-    const bool mine = t < T && (bitmap[static_cast<int64_t>(t) * words + (e >> 5)] & bit);
-    const uint64_t mask = __ballot(mine);
-    if (mine) {
-      const int rank = running + __popcll(mask & ((1ull << lane) - 1ull));
-      const int pos = before + rank;
-      int s = 0;
-      while (s < k && ids[static_cast<int64_t>(t) * k + s] != e) ++s;
-      if (s < k) {
-        perm[pos] = t * k + s;
-        inv[t * k + s] = pos;
-      }
+    const int slot1 = t < p.T ? row[t] : 0;
+    const uint64_t mask = __ballot(slot1 != 0);
+    if (slot1) {
+      const int pos = before + running + __popcll(mask & ((1ull << lane) - 1ull));
+      const int flat = t * p.k + slot1 - 1;
+      p.perm[pos] = flat;
+      p.inv[flat] = pos;
     }
     running += __popcll(mask);
   }
 }
 
 // ---------------------------------------------------------------------------
-// Hit list from existing segment offsets (experts with a nonempty segment, in
-// ascending order).  block = 1024, E <= 1024.
-__global__ __launch_bounds__(1024) void hitlist_kernel(const int32_t* __restrict__ offsets, int E,
-                                                       int32_t* __restrict__ hit, int32_t* __restrict__ meta) {
-  __shared__ int wave_nz[16];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id();
-  const int nonempty = (tid < E && offsets[tid + 1] > offsets[tid]) ? 1 : 0;
-  int incl = nonempty;
-  for (int o = 1; o < 64; o <<= 1) {
-    const int a = __shfl_up(incl, o, 64);
-    if (lane >= o) incl += a;
+// Work table from existing segment offsets (experts-only entry) plus the
+// activation prep rows.  block = 512: block 0 builds the table (E <= 1024
+// experts, two per thread), blocks 1..T prepare rows.
+__global__ __launch_bounds__(512) void table_prep_kernel(TableParams p) {
+  if (blockIdx.x > 0) {
+    prep_row(p.x, p.H, blockIdx.x - 1, p.x_il, p.xneg, p.gate_w, p.gate_out);
+    return;
   }
-  if (lane == 63) wave_nz[wave] = incl;
+  __shared__ int wave_tot[2][8];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id();
+  int cnt[2], b = 0, c = 0;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int e = 2 * tid + j;
+    cnt[j] = e < p.E ? p.offsets[e + 1] - p.offsets[e] : 0;
+    b += cnt[j] > 0 ? 1 : 0;
+    c += passes_for(cnt[j], p.rows_per_pass);
+  }
+  int ib = b, ic = c;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int ub = __shfl_up(ib, o, 64), uc = __shfl_up(ic, o, 64);
+    if (lane >= o) {
+      ib += ub;
+      ic += uc;
+    }
+  }
+  if (lane == 63) {
+    wave_tot[0][wave] = ib;
+    wave_tot[1][wave] = ic;
+  }
   __syncthreads();
-  int base = 0;
-  for (int i = 0; i < wave; ++i) base += wave_nz[i];
-  if (nonempty) hit[base + incl - 1] = tid;
-  if (tid == E - 1) meta[0] = base + incl;
+  int bb = 0, bc = 0;
+  for (int i = 0; i < wave; ++i) {
+    bb += wave_tot[0][i];
+    bc += wave_tot[1][i];
+  }
+  int h = bb + ib - b, ps = bc + ic - c;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int e = 2 * tid + j;
+    if (cnt[j] > 0) {
+      p.hit[h] = e;
+      p.pass_start[h] = ps;
+      write_slot(p.slot_table, p.pass_slot, h, e, p.offsets[e], cnt[j], ps, p.rows_per_pass);
+      ++h;
+    }
+    ps += passes_for(cnt[j], p.rows_per_pass);
+  }
+  if (tid == 511) {
+    int total = ps;
+    p.pass_start[h] = total;
+    if (p.has_shared) {
+      write_slot(p.slot_table, p.pass_slot, h, -1, 0, p.T, total, p.rows_per_pass);
+      total += passes_for(p.T, p.rows_per_pass);
+    }
+    p.pass_start[h + p.has_shared] = total;
+    p.meta[0] = h;
+    p.meta[1] = total;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -360,16 +444,12 @@ __global__ __launch_bounds__(1024) void hitlist_kernel(const int32_t* __restrict
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y, const int32_t* __restrict__ inv, int T,
                                                       int k, int H, int has_shared, uint16_t* __restrict__ out) {
   const int t = blockIdx.x;
+  const int nrows = k + (has_shared ? 1 : 0);
   for (int c = threadIdx.x * 8; c < H; c += 256 * 8) {
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < k; ++s) {
-      const float4* src = reinterpret_cast<const float4*>(y + static_cast<int64_t>(inv[t * k + s]) * H + c);
-      const float4 a = src[0], b = src[1];
-      acc[0] += a.x; acc[1] += a.y; acc[2] += a.z; acc[3] += a.w;
-      acc[4] += b.x; acc[5] += b.y; acc[6] += b.z; acc[7] += b.w;
-    }
-    if (has_shared) {
-      const float4* src = reinterpret_cast<const float4*>(y + (static_cast<int64_t>(T) * k + t) * H + c);
+    for (int s = 0; s < nrows; ++s) {
+      const int64_t row = s < k ? inv[t * k + s] : static_cast<int64_t>(T) * k + t;
+      const float4* src = reinterpret_cast<const float4*>(y + row * H + c);
       const float4 a = src[0], b = src[1];
       acc[0] += a.x; acc[1] += a.y; acc[2] += a.z; acc[3] += a.w;
       acc[4] += b.x; acc[5] += b.y; acc[6] += b.z; acc[7] += b.w;
@@ -385,39 +465,38 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 
 // ---------------------------------------------------------------------------
 // host launchers
-void launch_prep(const uint16_t* x, int rows, int K, int group, uint16_t* x_il, float* xneg, const uint16_t* gate_w,
-                 float* gate_out, hipStream_t stream) {
-  if (rows <= 0) return;
-  hipLaunchKernelGGL(prep_kernel, dim3(rows), dim3(256), 0, stream, x, K, group, x_il, xneg, gate_w, gate_out);
-}
-
-void launch_router(const uint16_t* x, const uint16_t* w, float* logits, int T, int E, int H, hipStream_t stream) {
-  if (T <= 0) return;
-  hipLaunchKernelGGL(router_kernel, dim3((T + 15) / 16, (E + 15) / 16), dim3(512), 0, stream, x, w, logits, T, E, H);
+void launch_front(const FrontParams& p, hipStream_t stream) {
+  const int blocks = p.n_router + p.prep_rows + p.n_zero;
+  if (blocks <= 0) return;
+  hipLaunchKernelGGL(front_kernel, dim3(blocks), dim3(512), 0, stream, p);
 }
 
 bool route_small_fits(int T, int E, int k) {
-  return static_cast<int64_t>(T) * k <= kSmallPairs && static_cast<int64_t>(T) * ((E + 31) / 32) <= kSmallBitmapWords;
+  return static_cast<int64_t>(T) * k <= kSmallPairs && static_cast<int64_t>((T + 3) & ~3) * E <= kSmallSlotBytes;
 }
 
-void launch_route(const float* logits, int T, int E, int k, int32_t* ids, float* wts, int32_t* perm, int32_t* inv,
-                  int32_t* offsets, int32_t* hit, int32_t* meta, int32_t* counts, uint32_t* bitmap, bool allow_small,
-                  hipStream_t stream) {
-  if (allow_small && route_small_fits(T, E, k)) {
-    hipLaunchKernelGGL(route_small_kernel, dim3(1), dim3(1024), 0, stream, logits, T, E, k, ids, wts, perm, inv, offsets,
-                       hit, meta);
+int64_t route_zero_words(int T, int E) {
+  // counts [E] followed by the slot map [E][T] bytes, in 32-bit words
+  return E + (static_cast<int64_t>(E) * T + 3) / 4;
+}
+
+void launch_route(const RouteParams& p, bool zeroed, hipStream_t stream) {
+  if (route_small_fits(p.T, p.E, p.k)) {
+    hipLaunchKernelGGL(route_small_kernel, dim3(1), dim3(1024), 0, stream, p);
     return;
   }
-  hipLaunchKernelGGL(route_zero_kernel, dim3(1), dim3(256), 0, stream, counts, E);
-  if (T > 0)
-    hipLaunchKernelGGL(route_topk_kernel, dim3((T + 3) / 4), dim3(256), 0, stream, logits, T, E, k, ids, wts, counts,
-                       bitmap);
-  hipLaunchKernelGGL(route_permute_kernel, dim3((E + 3) / 4), dim3(256), 0, stream, ids, counts, bitmap, T, E, k, perm,
-                     inv, offsets, hit, meta);
+  if (!zeroed) {
+    const int64_t words = route_zero_words(p.T, p.E);
+    const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((words + 255) / 256, 1024));
+    hipLaunchKernelGGL(route_zero_kernel, dim3(blocks), dim3(256), 0, stream,
+                       reinterpret_cast<uint32_t*>(p.counts), words);
+  }
+  if (p.T > 0) hipLaunchKernelGGL(route_topk_kernel, dim3((p.T + 3) / 4), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL(route_permute_kernel, dim3((p.E + 3) / 4), dim3(256), 0, stream, p);
 }
 
-void launch_hitlist(const int32_t* offsets, int E, int32_t* hit, int32_t* meta, hipStream_t stream) {
-  hipLaunchKernelGGL(hitlist_kernel, dim3(1), dim3(1024), 0, stream, offsets, E, hit, meta);
+void launch_table_prep(const TableParams& p, hipStream_t stream) {
+  hipLaunchKernelGGL(table_prep_kernel, dim3(1 + p.T), dim3(512), 0, stream, p);
 }
 
 void launch_combine(const float* y, const int32_t* inv, int T, int k, int H, int has_shared, uint16_t* out,

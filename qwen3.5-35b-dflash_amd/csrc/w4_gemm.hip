@@ -1,4 +1,6 @@
-// Small-M grouped W4A16 GEMM on v_mfma_f32_16x16x32_bf16 (verify-block path).
+// Per-wave grouped W4A16 GEMM on v_mfma_f32_16x16x32_bf16: the general
+// fallback for reduction lengths the streaming kernel does not split
+// (any K % 512 == 0).
 //
 // One wave owns a 32-row strip of one weight matrix (two 16-row MFMA column
 // tiles) and streams it once per pass over up to 32 of the slot's token rows.
@@ -18,7 +20,7 @@
 namespace dflash {
 
 template <int kMode, int kMT, typename ScaleT>
-__device__ __forceinline__ void w4_pass(const W4GemmParams& p, const uint8_t* __restrict__ w,
+__device__ __forceinline__ void w4_pass(const W4StreamParams& p, const uint8_t* __restrict__ w,
                                         const ScaleT* __restrict__ s, int seg, int M, int m0, bool shared, int row0,
                                         int row1, int strip) {
   const int lane = lane_id(), lr = lane & 15, kq = lane >> 4;
@@ -100,13 +102,10 @@ __device__ __forceinline__ void w4_pass(const W4GemmParams& p, const uint8_t* __
     for (int mt = 0; mt < kMT; ++mt) {
       float xv = 0.f;
       if (ok) {
-        if (kMode == kModeDown) {
-          const int parts = G >> 4;
-          const float* src = p.act_neg + static_cast<int64_t>(arow[mt]) * (K >> 4) + g * parts;
-          for (int c = 0; c < parts; ++c) xv += src[c];
-        } else {
-          xv = p.act_neg[static_cast<int64_t>(arow[mt]) * ngroups + g];
-        }
+        // act_neg holds neg_parts partial sums per 128-column block; a group spans spg blocks
+        const int parts = spg * p.neg_parts;
+        const float* src = p.act_neg + static_cast<int64_t>(arow[mt]) * nkb * p.neg_parts + g * parts;
+        for (int c = 0; c < parts; ++c) xv += src[c];
       }
       tot0[mt] = mfma16x16x4f32(xv, sv0, tot0[mt]);
       tot1[mt] = mfma16x16x4f32(xv, sv1, tot1[mt]);
@@ -148,11 +147,12 @@ __device__ __forceinline__ void w4_pass(const W4GemmParams& p, const uint8_t* __
 }
 
 template <int kMode, typename ScaleT>
-__global__ __launch_bounds__(256) void w4_gemm_kernel(W4GemmParams p) {
+__global__ __launch_bounds__(256) void w4_gemm_kernel(W4StreamParams p, int max_slots) {
+  const int items_per_slot = p.N >> 5;  // gate_up: I/16 column pairs; down, linear: 32-row strips
   const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int slot = item / p.items_per_slot;
-  const int strip = item - slot * p.items_per_slot;
-  if (slot >= p.max_slots) return;
+  const int slot = item / items_per_slot;
+  const int strip = item - slot * items_per_slot;
+  if (slot >= max_slots) return;
   const uint8_t* w;
   const ScaleT* s;
   int seg = 0, M;
@@ -197,13 +197,13 @@ __global__ __launch_bounds__(256) void w4_gemm_kernel(W4GemmParams p) {
   }
 }
 
-void launch_w4_gemm(int mode, bool fp32_scales, const W4GemmParams& p, hipStream_t stream) {
-  const int64_t items = static_cast<int64_t>(p.max_slots) * p.items_per_slot;
+void launch_w4_gemm(int mode, bool fp32_scales, int max_slots, const W4StreamParams& p, hipStream_t stream) {
+  const int64_t items = static_cast<int64_t>(max_slots) * (p.N >> 5);
   if (items <= 0) return;
   const dim3 grid(static_cast<unsigned>((items + 3) / 4)), block(256);
-#define DFLASH_W4_LAUNCH(MODE)                                                              \
-  if (fp32_scales) hipLaunchKernelGGL((w4_gemm_kernel<MODE, float>), grid, block, 0, stream, p); \
-  else hipLaunchKernelGGL((w4_gemm_kernel<MODE, uint16_t>), grid, block, 0, stream, p);
+#define DFLASH_W4_LAUNCH(MODE)                                                                          \
+  if (fp32_scales) hipLaunchKernelGGL((w4_gemm_kernel<MODE, float>), grid, block, 0, stream, p, max_slots); \
+  else hipLaunchKernelGGL((w4_gemm_kernel<MODE, uint16_t>), grid, block, 0, stream, p, max_slots);
   switch (mode) {
     case kModeLinear: DFLASH_W4_LAUNCH(kModeLinear) break;
     case kModeGateUp: DFLASH_W4_LAUNCH(kModeGateUp) break;

@@ -1,0 +1,147 @@
+"""CPU: the C-ABI library loads, exports every declared symbol, and validates arguments.
+
+No call here reaches a kernel launch: every invocation fails argument
+validation on the host (or is a pure size query), so no GPU is touched.
+"""
+import ctypes
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "dflash_hip.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(dflash_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_binding_table(pkg):
+    assert _declared_functions() == sorted(pkg._lib.SIGNATURES)
+
+
+def test_library_loads_and_exports_every_symbol(pkg):
+    lib = pkg._lib.load()
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.dflash_abi_version() == pkg._lib.ABI_VERSION == 1
+
+
+def test_library_has_no_unresolved_internal_symbols(pkg):
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    out = subprocess.run([nm, "-D", "--undefined-only", str(pkg._lib.LIBRARY_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    assert "dflash" not in out, out
+
+
+@pytest.mark.parametrize("compiler,lang", [("gcc", "c"), ("g++", "c++")])
+def test_header_compiles_standalone(compiler, lang, tmp_path):
+    exe = shutil.which(compiler)
+    if exe is None:
+        pytest.skip(f"{compiler} not available")
+    src = tmp_path / ("probe.c" if lang == "c" else "probe.cc")
+    src.write_text('#include "dflash_hip.h"\nint main(void) { dflash_w4 w; (void)w; return DFLASH_ABI_VERSION; }\n')
+    subprocess.run([exe, "-x", lang, "-Wall", "-Wextra", "-Werror", "-I", str(HEADER.parent), "-fsyntax-only",
+                    str(src)], check=True)
+
+
+host_only = pytest.mark.skipif(
+    __import__("torch").cuda.is_available(),
+    reason="passes fake device pointers that must fail host validation; run only where no GPU is visible")
+
+
+def _desc(pkg, experts=1, rows=512, cols=2048, group=128, dtype=0, packed=16, scales=16):
+    return pkg._lib.W4Desc(packed=packed, scales=scales, experts=experts, rows=rows, cols=cols, group_size=group,
+                           scale_dtype=dtype)
+
+
+def _status(pkg, name, *args):
+    lib = pkg._lib.load()
+    return getattr(lib, name)(*args), lib.dflash_last_error().decode()
+
+
+@host_only
+def test_qlinear_validation(pkg):
+    ws = ctypes.c_void_p(4096)
+    st, msg = _status(pkg, "dflash_qlinear_w4a16", ctypes.c_void_p(16), 16, None, ctypes.c_void_p(16), ws, 1 << 20, None)
+    assert st == 1 and "NULL" in msg
+    d = _desc(pkg, group=64)
+    st, msg = _status(pkg, "dflash_qlinear_w4a16", ctypes.c_void_p(16), 16, ctypes.byref(d), ctypes.c_void_p(16), ws,
+                      1 << 20, None)
+    assert st == 2 and "group_size" in msg
+    d = _desc(pkg, rows=48)
+    st, msg = _status(pkg, "dflash_qlinear_w4a16", ctypes.c_void_p(16), 16, ctypes.byref(d), ctypes.c_void_p(16), ws,
+                      1 << 20, None)
+    assert st == 2 and "N % 32" in msg
+    d = _desc(pkg, packed=17)
+    st, msg = _status(pkg, "dflash_qlinear_w4a16", ctypes.c_void_p(16), 16, ctypes.byref(d), ctypes.c_void_p(16), ws,
+                      1 << 20, None)
+    assert st == 1 and "aligned" in msg
+    d = _desc(pkg)
+    st, msg = _status(pkg, "dflash_qlinear_w4a16", ctypes.c_void_p(16), 16, ctypes.byref(d), ctypes.c_void_p(16), ws,
+                      16, None)
+    assert st == 3 and "workspace" in msg
+    st, _ = _status(pkg, "dflash_qlinear_w4a16", None, 0, ctypes.byref(d), None, None, 0, None)
+    assert st == 0  # m == 0 is a no-op
+
+
+@host_only
+def test_route_validation(pkg):
+    p = ctypes.c_void_p(16)
+    st, msg = _status(pkg, "dflash_moe_route", p, 16, 2048, 8, p, p, p, p, p, p, 1 << 20, None)
+    assert st == 2 and "experts" in msg
+    st, msg = _status(pkg, "dflash_moe_route", p, 16, 256, 0, p, p, p, p, p, p, 1 << 20, None)
+    assert st == 1 and "top_k" in msg
+    st, msg = _status(pkg, "dflash_moe_route", p, 16, 256, 8, p, p, p, p, None, p, 1 << 20, None)
+    assert st == 1 and "expert_offsets" in msg
+    st, msg = _status(pkg, "dflash_moe_route", p, 16, 256, 8, p, p, p, p, p, p, 8, None)
+    assert st == 3
+
+
+@host_only
+def test_moe_validation(pkg):
+    p = ctypes.c_void_p(16)
+    gu = _desc(pkg, experts=256, rows=1024, cols=2048)
+    dn = _desc(pkg, experts=256, rows=2048, cols=512)
+    bad_dn = _desc(pkg, experts=256, rows=2048, cols=1024)
+    lib = pkg._lib.load()
+    args = lambda g, d, k=8, h=2048: (p, 16, h, None, p, k, ctypes.byref(g), ctypes.byref(d), None, None, None,  # noqa: E731
+                                      p, None, p, p, p, p, p, p, 1 << 30, None)
+    assert lib.dflash_moe_w4a16(*args(gu, bad_dn)) == 1
+    assert "down" in lib.dflash_last_error().decode()
+    assert lib.dflash_moe_w4a16(*args(gu, dn, k=300)) == 1
+    assert lib.dflash_moe_w4a16(*args(gu, dn, h=1000)) == 2
+    shared_only_gate = (p, 16, 2048, None, p, 8, ctypes.byref(gu), ctypes.byref(dn), None, None, p,
+                        p, None, p, p, p, p, p, p, 1 << 30, None)
+    assert lib.dflash_moe_w4a16(*shared_only_gate) == 1
+    assert "shared" in lib.dflash_last_error().decode()
+    small_ws = (p, 16, 2048, None, p, 8, ctypes.byref(gu), ctypes.byref(dn), None, None, None,
+                p, None, p, p, p, p, p, p, 64, None)
+    assert lib.dflash_moe_w4a16(*small_ws) == 3
+
+
+def test_workspace_queries(pkg):
+    lib = pkg._lib.load()
+    a = lib.dflash_moe_workspace_bytes(16, 2048, 512, 256, 8, 128, 1)
+    b = lib.dflash_moe_workspace_bytes(2048, 2048, 512, 256, 8, 128, 1)
+    assert 0 < a < b
+    assert lib.dflash_moe_workspace_bytes(-1, 2048, 512, 256, 8, 128, 1) == 0
+    assert lib.dflash_qlinear_workspace_bytes(16, 2048, 128) >= 16 * 2048 * 2
+    assert lib.dflash_moe_route_workspace_bytes(16, 256, 8) > 0
+
+
+def test_python_wrappers_refuse_cpu_tensors(pkg):
+    """No CPU fallback: the HIP entry points reject host tensors before any launch."""
+    import torch
+    w = pkg.synthetic.int4_weight(torch.Generator().manual_seed(0), (64, 512))
+    x = torch.zeros((4, 512), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="ROCm device"):
+        pkg.ops.qlinear(x, w)
+    with pytest.raises(ValueError, match="ROCm device"):
+        pkg.ops.route(torch.zeros((4, 16)), 2)
