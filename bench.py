@@ -12,9 +12,12 @@ multi-layer verify forward would be issued), so host launch overhead is not
 part of the measurement.
 
 Prints ONE JSON line.  ``value`` is microseconds per MoE layer (lower is
-better).  ``roofline`` is the expert stage (the kernels that stream the int4
-expert weights), timed with HIP events on the launch stream:
-achieved = int4 weight bytes of the hit experts + shared expert / time.
+better).  ``roofline`` is the dominant kernel, the grouped gate/up GEMM:
+HIP events on its launch stream bracket graph replays that hold only that
+kernel's launches (measurement mode of the library), one per step over the
+same rotation of weight sets and hidden blocks; achieved = its algorithmic
+bytes (int4 gate/up rows + bf16 scales of the hit experts and the shared
+expert, x in, h out) / mean launch duration.
 ``prefill`` reports the T=2048 layer in TFLOP/s against bf16 MFMA peak.
 ``cpu_baseline`` times the oracle's CPU restatement of the same layer.
 """
@@ -147,6 +150,45 @@ def time_experts(pkg, sets, blocks, top_k, steps, warmup, workspace):
     return ms, statistics.mean(p[5] for p in prepared)
 
 
+GATE_UP_BYTES_PER_EXPERT = 2 * 512 * 2048 // 2 + 2 * 512 * (2048 // 128) * 2   # int4 + bf16 scales
+
+
+def time_stage(pkg, sets, blocks, top_k, steps, warmup, stage=None):
+    """Average launch duration of one expert-stage kernel, timed with HIP events.
+
+    For each of `period` steps (weight set j % sets, hidden block j % blocks)
+    a full layer call fills its own workspace; then, in measurement mode,
+    layer calls launch only the stage's kernel on that workspace.  A HIP graph
+    of those single-kernel steps is replayed between two events on torch's
+    current stream (the stream the library launches on), so the timed region
+    holds nothing but back-to-back launches of the kernel.  Returns the mean
+    duration per launch (ms) and the mean number of hit experts.
+    """
+    stage = pkg.ops.STAGE_GATE_UP if stage is None else stage
+    period = 24
+    device = blocks[0].device
+    nbytes = pkg.ops.moe_workspace_bytes(blocks[0].shape[0], 2048, 512, 256, top_k, 128, True)
+    wss = [torch.empty(nbytes, dtype=torch.uint8, device=device) for _ in range(period)]
+    hits = []
+    for j in range(period):
+        gu, dn, sh, router = sets[j % len(sets)]
+        _, r, _ = pkg.ops.moe_w4a16(blocks[j % len(blocks)], gu, dn, top_k=top_k, router_weight=router, shared=sh,
+                                    workspace=wss[j], return_routing=True)
+        hits.append(int((r.offsets[1:] > r.offsets[:-1]).sum().item()))
+    torch.cuda.synchronize()
+
+    def step(j):
+        gu, dn, sh, router = sets[j % len(sets)]
+        pkg.ops.moe_w4a16(blocks[j % len(blocks)], gu, dn, top_k=top_k, router_weight=router, shared=sh,
+                          workspace=wss[j % period])
+    pkg.ops.set_measure_stage(stage)
+    try:
+        ms = time_steps(step, steps, warmup, period)
+    finally:
+        pkg.ops.set_measure_stage(0)
+    return ms, statistics.mean(hits)
+
+
 def cpu_baseline(pkg, tokens, top_k, seconds_budget=20.0):
     """Oracle CPU restatement of the same layer (dense bf16 banks of the hit experts), median of timed runs."""
     import numpy as np
@@ -196,7 +238,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (the MoE layer would shard by "
-              "expert parallelism, see DESIGN.md)", file=sys.stderr)
+              "expert parallelism)", file=sys.stderr)
         return 2
     pkg = load_package()
     assert torch.cuda.is_available(), "bench.py needs a ROCm device"
@@ -217,8 +259,14 @@ def main() -> int:
     exp_ms, hits = time_experts(pkg, sets, blocks, top_k, args.steps, args.warmup, ws)
     int4_bytes = (hits + 1) * INT4_BYTES_PER_EXPERT
     all_bytes = (hits + 1) * (INT4_BYTES_PER_EXPERT + SCALE_BYTES_PER_EXPERT)
-    achieved = int4_bytes / (exp_ms * 1e-3) / 1e9
     layer_gbs = int4_bytes / (ms * 1e-3) / 1e9
+    log("timing the gate/up kernel with HIP events")
+    gu_ms, gu_hits = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup)
+    dn_ms, _ = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup, pkg.ops.STAGE_DOWN)
+    # algorithmic bytes of one gate/up launch: the hit experts' and the shared
+    # expert's int4 gate/up rows + bf16 scales, x read, h (bf16) written
+    gu_bytes = (gu_hits + 1) * GATE_UP_BYTES_PER_EXPERT + tokens * 2048 * 2 + (tokens * top_k + tokens) * 512 * 2
+    achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
 
     result = {
         "metric": METRIC, "value": round(ms * 1e3, 2), "unit": "us/layer", "n_gpus": 1,
@@ -234,9 +282,12 @@ def main() -> int:
         "layer_hbm_frac_int4": round(layer_gbs / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "expert stage (prep, hitlist, w4_gemm gate_up, w4_gemm down, combine)",
-                     "stage_us": round(exp_ms * 1e3, 2), "hit_experts_mean": round(hits, 2),
-                     "int4_bytes_per_launch": int(int4_bytes), "all_weight_bytes_per_launch": int(all_bytes)},
+                     "kernel": "w4_wave_kernel<1, 16, unsigned short> (grouped gate/up + SiLU*up, T=16)",
+                     "kernel_us": round(gu_ms * 1e3, 2), "hit_experts_mean": round(gu_hits, 2),
+                     "bytes_per_launch": int(gu_bytes)},
+        "stages": {"expert_stage_us": round(exp_ms * 1e3, 2), "down_kernel_us": round(dn_ms * 1e3, 2),
+                   "expert_int4_bytes": int(int4_bytes), "expert_weight_bytes": int(all_bytes),
+                   "expert_stage_int4_gbs": round(int4_bytes / (exp_ms * 1e-3) / 1e9, 1)},
     }
     if not args.no_prefill:
         log("timing the T=2048 prefill layer")

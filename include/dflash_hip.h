@@ -130,6 +130,23 @@ int dflash_moe_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, co
                      int32_t* inv_perm, int32_t* expert_offsets, void* workspace, size_t workspace_bytes,
                      void* stream);
 
+/*
+ * Measurement mode (no counterpart in the reference; for benchmarks and
+ * profilers that time one kernel of the layer on its own): while a stage is
+ * set, dflash_moe_w4a16 and dflash_moe_experts_w4a16 validate their arguments
+ * as usual but launch only that stage's kernel, which reads the routing, work
+ * table and intermediate activations that an earlier full call with the same
+ * arguments left in the same workspace, and writes the same intermediate
+ * output again (out is not written).  DFLASH_STAGE_NONE restores full calls.
+ * Process-wide.
+ */
+enum dflash_stage {
+  DFLASH_STAGE_NONE = 0,
+  DFLASH_STAGE_GATE_UP = 1, /* grouped gate/up GEMM + SiLU*up of the expert FFN */
+  DFLASH_STAGE_DOWN = 2     /* grouped down GEMM + routing weight of the expert FFN */
+};
+int dflash_set_measure_stage(int stage);
+
 #ifdef __cplusplus
 }
 #endif

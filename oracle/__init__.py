@@ -1,6 +1,6 @@
 """CPU oracle for the W4A16 qlinear and routed-MoE expert FFN.
 
-TEST INFRASTRUCTURE ONLY.  This package is the checker: only ``tests/``,
+TEST INFRASTRUCTURE ONLY.  This package is the oracle the tests check against: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
 import it.  The product path (``qwen3.5-35b-dflash_amd``) never imports, links
 or falls back to anything here.

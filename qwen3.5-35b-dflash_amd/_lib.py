@@ -58,7 +58,12 @@ SIGNATURES = {
                                                 _P, _P, _P, _SZ, _P]),
     "dflash_moe_w4a16": (ctypes.c_int, [_P, _I64, _I64, _P, _P, _I64, _W4P, _W4P, _W4P, _W4P, _P, _P, _P, _P, _P,
                                         _P, _P, _P, _P, _SZ, _P]),
+    "dflash_set_measure_stage": (ctypes.c_int, [ctypes.c_int]),
 }
+
+STAGE_NONE = 0
+STAGE_GATE_UP = 1
+STAGE_DOWN = 2
 
 
 class DflashError(RuntimeError):

@@ -60,7 +60,7 @@ int check_w4(const dflash_w4* w, const char* name, int64_t experts, int64_t rows
 
 // ---------------------------------------------------------------- layouts
 struct RouteLayout {
-  size_t meta, hit, pass_start, slot_table, pass_slot, counts, slotmap, total;
+  size_t meta, hit, pass_start, slot_table, pass_slot, pass_table, slot_w, tok, counts, slotmap, total;
 };
 
 RouteLayout route_layout(int64_t T, int64_t k, int64_t E) {
@@ -71,6 +71,9 @@ RouteLayout route_layout(int64_t T, int64_t k, int64_t E) {
   L.pass_start = c.take(4 * static_cast<size_t>(E + 4));
   L.slot_table = c.take(16 * static_cast<size_t>(E + 2));
   L.pass_slot = c.take(4 * static_cast<size_t>(T * k + T + 4));  // a pass holds at least one row
+  L.pass_table = c.take(16 * static_cast<size_t>(T * k + T + 4));
+  L.slot_w = c.take(4 * static_cast<size_t>(T * k + 1));
+  L.tok = c.take(4 * static_cast<size_t>(T * k + 1));
   // counts and the slot map are contiguous: one clearing pass covers both
   L.counts = c.off;
   L.slotmap = L.counts + 4 * static_cast<size_t>(E);
@@ -120,6 +123,10 @@ int cu_count() {
 
 int token_tiles(int64_t T) { return T <= 16 ? 1 : 2; }
 
+// Small token counts run both expert GEMMs on the wave-streaming kernel, whose
+// passes hold 16 rows; larger T uses passes of 16 * token_tiles(T) rows.
+constexpr int64_t kWaveMaxTokens = 32;
+
 int check_route_args(int64_t T, int64_t E, int64_t k) {
   if (T < 0) return fail(DFLASH_ERR_INVALID_ARGUMENT, "tokens must be >= 0");
   if (T > (1 << 24)) return fail(DFLASH_ERR_UNSUPPORTED, "tokens above 2^24 are not supported");
@@ -130,10 +137,20 @@ int check_route_args(int64_t T, int64_t E, int64_t k) {
 }
 
 struct MoeShapes {
-  int64_t T, H, I, E, k, G;
+  int64_t T, H, I, E, k, G, Gd;  // Gd: group size of the down bank
   bool shared;
   bool gu_f32, dn_f32;
+  bool scales16;  // every scale bank 16-byte aligned (row scales load as 16-byte words)
 };
+
+bool moe_wave_path(const MoeShapes& S) {
+  using namespace dflash;
+  return S.T <= kWaveMaxTokens && S.T * S.k <= kWaveMaxTokenRows && S.G == 128 && S.Gd == 128 && S.scales16 &&
+         w4_wave_supports(kModeGateUp, static_cast<int>(S.H), 128, static_cast<int>(S.T)) &&
+         w4_wave_supports(kModeDown, static_cast<int>(S.I), 128, 0);
+}
+
+int rows_per_pass(const MoeShapes& S) { return moe_wave_path(S) ? 16 : 16 * token_tiles(S.T); }
 
 int check_moe(const void* hidden, int64_t T, int64_t H, int64_t k, const dflash_w4* gate_up, const dflash_w4* down,
               const dflash_w4* sgu, const dflash_w4* sdn, const void* sgate, const void* out, MoeShapes* S) {
@@ -159,16 +176,35 @@ int check_moe(const void* hidden, int64_t T, int64_t H, int64_t k, const dflash_
   }
   if (T > 0 && (!hidden || !out)) return fail(DFLASH_ERR_INVALID_ARGUMENT, "hidden and out are required");
   if (!aligned16(hidden) || !aligned16(out)) return fail(DFLASH_ERR_INVALID_ARGUMENT, "hidden/out not 16-byte aligned");
-  *S = MoeShapes{T, H, I, E, k, gate_up->group_size, shared, gate_up->scale_dtype == DFLASH_DTYPE_F32,
-                 down->scale_dtype == DFLASH_DTYPE_F32};
+  const bool scales16 = aligned16(gate_up->scales) && aligned16(down->scales) &&
+                        (!shared || (aligned16(sgu->scales) && aligned16(sdn->scales)));
+  *S = MoeShapes{T, H, I, E, k, gate_up->group_size, down->group_size, shared,
+                 gate_up->scale_dtype == DFLASH_DTYPE_F32, down->scale_dtype == DFLASH_DTYPE_F32, scales16};
   return DFLASH_OK;
 }
 
-// One W4 GEMM over the work table: the streaming kernel when it splits this K
-// evenly, the per-wave kernel otherwise.
-void launch_w4(int mode, bool fp32_scales, int mt, int max_slots, dflash::W4StreamParams& p, hipStream_t stream) {
+// Stage of dflash_set_measure_stage (process-wide): when set, the MoE entry
+// points launch only that stage's kernel.
+std::atomic<int> g_measure{DFLASH_STAGE_NONE};
+
+bool measuring() { return g_measure.load(std::memory_order_acquire) != DFLASH_STAGE_NONE; }
+bool stage_on(int stage) {
+  const int m = g_measure.load(std::memory_order_acquire);
+  return m == DFLASH_STAGE_NONE || m == stage;
+}
+
+// One W4 GEMM over the work table: the wave-streaming kernel for small T
+// (wave == true), else the workgroup-streaming kernel when it splits this K
+// evenly, else the per-wave fallback.
+void launch_w4(int mode, bool fp32_scales, int mt, int max_slots, bool wave, dflash::W4StreamParams& p,
+               hipStream_t stream) {
   using namespace dflash;
   const int cols = mode == kModeGateUp ? p.N / 2 / 16 : p.N / 32;  // 16-column pairs or 32-row strips
+  if (wave) {
+    p.strips = cols;
+    launch_w4_wave(mode, fp32_scales, cu_count(), p, stream);
+    return;
+  }
   const int rg = w4_stream_row_groups(p.K);
   if (w4_stream_supports(p.K, p.G) && cols % rg == 0) {
     p.strips = cols / rg;
@@ -179,19 +215,21 @@ void launch_w4(int mode, bool fp32_scales, int mt, int max_slots, dflash::W4Stre
 }
 
 // gate_up -> down -> combine for a routing and work table already in place.
-int run_experts(const MoeShapes& S, const float* topk_weights, const int32_t* perm, const int32_t* inv,
-                const int32_t* offsets, const int32_t* hit, const int32_t* pass_start, const int32_t* meta,
-                const int4* slot_table, const int32_t* pass_slot, const dflash_w4* gate_up, const dflash_w4* down, const dflash_w4* sgu, const dflash_w4* sdn,
-                void* out, void* ws, const MoeLayout& L, hipStream_t stream) {
+// Every kernel input besides x and the weight banks comes from the workspace
+// (routing kernels or table_prep wrote it); inv (the caller's) feeds combine.
+int run_experts(const MoeShapes& S, const int32_t* inv, void* ws, const MoeLayout& L, const dflash_w4* gate_up,
+                const dflash_w4* down, const dflash_w4* sgu, const dflash_w4* sdn, void* out, hipStream_t stream) {
   using namespace dflash;
   const int T = static_cast<int>(S.T), H = static_cast<int>(S.H), I = static_cast<int>(S.I);
   const int k = static_cast<int>(S.k);
-  const int mt = token_tiles(S.T);
+  const bool wave = moe_wave_path(S);
+  const int mt = wave ? 1 : token_tiles(S.T);
+  const int32_t* meta = at<int32_t>(ws, L.route.meta);
+  const int4* slot_table = at<int4>(ws, L.route.slot_table);
+  const int32_t* pass_slot = at<int32_t>(ws, L.route.pass_slot);
   W4StreamParams p{};
-  p.perm = perm;
-  p.offsets = offsets;
-  p.hit = hit;
-  p.pass_start = pass_start;
+  p.pass_table = at<int4>(ws, L.route.pass_table);
+  p.tok = at<int32_t>(ws, L.route.tok);
   p.meta = meta;
   p.slot_table = slot_table;
   p.pass_slot = pass_slot;
@@ -216,7 +254,7 @@ int run_experts(const MoeShapes& S, const float* topk_weights, const int32_t* pe
   p.neg_parts = 1;
   p.out_bf16 = at<uint16_t>(ws, L.h);
   p.out_part = at<float>(ws, L.hpart);
-  launch_w4(kModeGateUp, S.gu_f32, mt, max_slots, p, stream);
+  if (stage_on(DFLASH_STAGE_GATE_UP)) launch_w4(kModeGateUp, S.gu_f32, mt, max_slots, wave, p, stream);
   if (int r = launch_status("gate_up")) return r;
 
   // down: N = H rows over K = I, routing-weight epilogue into y
@@ -235,11 +273,12 @@ int run_experts(const MoeShapes& S, const float* topk_weights, const int32_t* pe
   p.out_bf16 = nullptr;
   p.out_part = nullptr;
   p.out_f32 = at<float>(ws, L.y);
-  p.route_w = topk_weights;
+  p.slot_w = at<float>(ws, L.route.slot_w);
   p.shared_gate = at<float>(ws, L.gate);
-  launch_w4(kModeDown, S.dn_f32, mt, max_slots, p, stream);
+  if (stage_on(DFLASH_STAGE_DOWN)) launch_w4(kModeDown, S.dn_f32, mt, max_slots, wave, p, stream);
   if (int r = launch_status("down")) return r;
 
+  if (measuring()) return DFLASH_OK;
   launch_combine(at<float>(ws, L.y), inv, T, k, H, p.has_shared, static_cast<uint16_t*>(out), stream);
   return launch_status("combine");
 }
@@ -264,6 +303,9 @@ dflash::RouteParams route_params(const float* logits, int64_t T, int64_t E, int6
   r.slotmap = at<uint8_t>(ws, L.slotmap);
   r.slot_table = at<int4>(ws, L.slot_table);
   r.pass_slot = at<int32_t>(ws, L.pass_slot);
+  r.pass_table = at<int4>(ws, L.pass_table);
+  r.slot_w = at<float>(ws, L.slot_w);
+  r.tok = at<int32_t>(ws, L.tok);
   r.rows_per_pass = rows_per_pass;
   r.has_shared = shared ? 1 : 0;
   return r;
@@ -324,9 +366,11 @@ int dflash_qlinear_w4a16(const void* x, int64_t m, const dflash_w4* weight, void
     p.neg_parts = 1;
     p.out_bf16 = static_cast<uint16_t*>(y);
     p.M = static_cast<int>(m);
-    const int mt = token_tiles(m);
+    const bool wave = aligned16(weight->scales) &&
+                      dflash::w4_wave_supports(dflash::kModeLinear, p.K, p.G, static_cast<int>(m));
+    const int mt = wave ? 1 : token_tiles(m);
     p.rows_per_pass = 16 * mt;
-    launch_w4(dflash::kModeLinear, weight->scale_dtype == DFLASH_DTYPE_F32, mt, 1, p, st);
+    launch_w4(dflash::kModeLinear, weight->scale_dtype == DFLASH_DTYPE_F32, mt, 1, wave, p, st);
     return launch_status("qlinear");
   } catch (...) {
     return fail(DFLASH_ERR_HIP, "unexpected host exception");
@@ -415,7 +459,13 @@ int dflash_moe_experts_w4a16(const void* hidden, int64_t tokens, int64_t hidden_
     t.meta = at<int32_t>(workspace, L.route.meta);
     t.slot_table = at<int4>(workspace, L.route.slot_table);
     t.pass_slot = at<int32_t>(workspace, L.route.pass_slot);
-    t.rows_per_pass = 16 * token_tiles(S.T);
+    t.pass_table = at<int4>(workspace, L.route.pass_table);
+    t.perm = perm;
+    t.wts = topk_weights;
+    t.slot_w = at<float>(workspace, L.route.slot_w);
+    t.tok = at<int32_t>(workspace, L.route.tok);
+    t.k = static_cast<int>(S.k);
+    t.rows_per_pass = rows_per_pass(S);
     t.has_shared = S.shared ? 1 : 0;
     t.x = static_cast<const uint16_t*>(hidden);
     t.H = static_cast<int>(S.H);
@@ -423,11 +473,9 @@ int dflash_moe_experts_w4a16(const void* hidden, int64_t tokens, int64_t hidden_
     t.xneg = at<float>(workspace, L.xneg);
     t.gate_w = S.shared ? static_cast<const uint16_t*>(shared_gate_weight) : nullptr;
     t.gate_out = at<float>(workspace, L.gate);
-    dflash::launch_table_prep(t, st);
+    if (!measuring()) dflash::launch_table_prep(t, st);
     if (int r = launch_status("table_prep")) return r;
-    return run_experts(S, topk_weights, perm, inv_perm, expert_offsets, t.hit, t.pass_start, t.meta, t.slot_table,
-                       t.pass_slot, gate_up, down,
-                       shared_gate_up, shared_down, out, workspace, L, st);
+    return run_experts(S, inv_perm, workspace, L, gate_up, down, shared_gate_up, shared_down, out, st);
   } catch (...) {
     return fail(DFLASH_ERR_HIP, "unexpected host exception");
   }
@@ -477,19 +525,24 @@ int dflash_moe_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, co
       f.zero_words = dflash::route_zero_words(T, E);
       f.n_zero = static_cast<int>(std::min<int64_t>(256, (f.zero_words + 2047) / 2048));
     }
-    dflash::launch_front(f, st);
+    if (!measuring()) dflash::launch_front(f, st);
     if (int r = launch_status("front")) return r;
     const dflash::RouteParams r = route_params(logits, S.T, S.E, S.k, topk_ids, topk_weights, perm, inv_perm,
-                                               expert_offsets, workspace, L.route, 16 * token_tiles(S.T), S.shared);
-    dflash::launch_route(r, true, st);
+                                               expert_offsets, workspace, L.route, rows_per_pass(S), S.shared);
+    if (!measuring()) dflash::launch_route(r, true, st);
     if (int rc = launch_status("route")) return rc;
     if (tokens == 0) return DFLASH_OK;
-    return run_experts(S, topk_weights, perm, inv_perm, expert_offsets, r.hit, r.pass_start, r.meta, r.slot_table,
-                       r.pass_slot, gate_up, down,
-                       shared_gate_up, shared_down, out, workspace, L, st);
+    return run_experts(S, inv_perm, workspace, L, gate_up, down, shared_gate_up, shared_down, out, st);
   } catch (...) {
     return fail(DFLASH_ERR_HIP, "unexpected host exception");
   }
+}
+
+int dflash_set_measure_stage(int stage) {
+  if (stage != DFLASH_STAGE_NONE && stage != DFLASH_STAGE_GATE_UP && stage != DFLASH_STAGE_DOWN)
+    return fail(DFLASH_ERR_INVALID_ARGUMENT, "unknown stage");
+  g_measure.store(stage, std::memory_order_release);
+  return DFLASH_OK;
 }
 
 }  // extern "C"

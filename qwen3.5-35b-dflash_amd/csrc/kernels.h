@@ -48,6 +48,9 @@ struct RouteParams {
   uint8_t* slotmap;     // [E][T]
   int4* slot_table;     // [E+1] per slot: expert (-1 shared), segment start, rows, first pass
   int32_t* pass_slot;   // [T*k + T] slot of every pass
+  int4* pass_table;     // [T*k + T] per pass: expert (-1 shared), segment start, slot rows, first row of the pass
+  float* slot_w;        // [T*k] routing weight of every slot row (wts[perm[i]])
+  int32_t* tok;         // [T*k] token of every slot row (perm[i] / k)
   int rows_per_pass;
   int has_shared;
 };
@@ -60,6 +63,12 @@ struct TableParams {
   int32_t* meta;
   int4* slot_table;
   int32_t* pass_slot;
+  int4* pass_table;
+  const int32_t* perm;
+  const float* wts;
+  float* slot_w;
+  int32_t* tok;
+  int k;
   int rows_per_pass, has_shared;
   // prep
   const uint16_t* x;
@@ -71,11 +80,14 @@ struct TableParams {
 };
 
 // Record slot `slot` (expert e, or -1 for the shared expert) in the work table.
-__device__ __forceinline__ void write_slot(int4* slot_table, int32_t* pass_slot, int slot, int e, int seg, int rows,
-                                           int pass0, int rows_per_pass) {
+__device__ __forceinline__ void write_slot(int4* slot_table, int32_t* pass_slot, int4* pass_table, int slot, int e,
+                                           int seg, int rows, int pass0, int rows_per_pass) {
   slot_table[slot] = make_int4(e, seg, rows, pass0);
   const int n = (rows + rows_per_pass - 1) / rows_per_pass;
-  for (int i = 0; i < n; ++i) pass_slot[pass0 + i] = slot;
+  for (int i = 0; i < n; ++i) {
+    pass_slot[pass0 + i] = slot;
+    pass_table[pass0 + i] = make_int4(e, seg, rows, i * rows_per_pass);
+  }
 }
 
 enum W4Mode : int { kModeLinear = 0, kModeGateUp = 1, kModeDown = 2 };
@@ -94,14 +106,12 @@ struct W4StreamParams {
   const uint16_t* act;
   const float* act_neg;
   int neg_parts;
-  // work table
-  const int32_t* perm;
-  const int32_t* offsets;
-  const int32_t* hit;
-  const int32_t* pass_start;
+  // work table (every input below lives in the workspace)
+  const int32_t* tok;      // token of every routed slot row [T*k]
   const int32_t* meta;
   const int4* slot_table;  // per slot: expert (-1 shared), segment start, rows, first pass
   const int32_t* pass_slot;
+  const int4* pass_table;  // per pass: expert (-1 shared), segment start, slot rows, first row of the pass
   int top_k, T, has_shared;
   int rows_per_pass;       // 16 * MT
   int strips;              // units per pass
@@ -109,7 +119,7 @@ struct W4StreamParams {
   uint16_t* out_bf16;      // kModeLinear: [M][N]; kModeGateUp: h [(T*k+T)][N/2] interleaved
   float* out_part;         // kModeGateUp: [(T*k+T)][N/32] partial -136*sum(h) per 16 columns
   float* out_f32;          // kModeDown: y [(T*k+T)][N]
-  const float* route_w;    // kModeDown: flat routing weights [T*k]
+  const float* slot_w;     // kModeDown: routing weight of every slot row [T*k]
   const float* shared_gate;// kModeDown: sigmoid gate [T]
   int M;                   // kModeLinear rows
 };
@@ -129,5 +139,10 @@ bool w4_stream_supports(int K, int G);
 int w4_stream_row_groups(int K);
 // mt: token tiles per pass (1 or 2); grid: persistent workgroups (one per CU)
 void launch_w4_stream(int mode, bool fp32_scales, int mt, int grid, const W4StreamParams& p, hipStream_t stream);
+// Wave-streaming kernel for small T (w4_wave.hip): 16-row passes, group 128, K in {512, 1024, 2048}.
+// rows: activation rows kept in LDS (T for gate_up, M for linear; ignored for down).
+bool w4_wave_supports(int mode, int K, int G, int rows);
+constexpr int kWaveMaxTokenRows = 2048;  // T * top_k routed slot rows whose tokens stay in LDS
+void launch_w4_wave(int mode, bool fp32_scales, int grid, const W4StreamParams& p, hipStream_t stream);
 
 }  // namespace dflash

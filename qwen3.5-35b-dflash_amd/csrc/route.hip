@@ -168,8 +168,19 @@ __device__ __forceinline__ void router_tile(const uint16_t* __restrict__ x, cons
   const uint16_t* xa = x + static_cast<int64_t>(trow) * H + wave * span + kq * 8;
   const uint16_t* wb = w + static_cast<int64_t>(erow) * H + wave * span + kq * 8;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int k = 0; k < span; k += 32)
-    acc = mfma16x16x32(*reinterpret_cast<const uint4*>(xa + k), *reinterpret_cast<const uint4*>(wb + k), acc);
+  // 8 MFMA steps per batch, all loads of a batch in flight together (span % 32 == 0)
+  for (int k0 = 0; k0 < span; k0 += 256) {
+    uint4 av[8], bv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int k = min(k0 + 32 * i, span - 32);
+      av[i] = *reinterpret_cast<const uint4*>(xa + k);
+      bv[i] = *reinterpret_cast<const uint4*>(wb + k);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (k0 + 32 * i < span) acc = mfma16x16x32(av[i], bv[i], acc);
+  }
   red[wave][lane] = acc;
   __syncthreads();
   if (wave == 0) {
@@ -214,6 +225,7 @@ __global__ __launch_bounds__(1024) void route_small_kernel(RouteParams p) {
   __shared__ int counts[kMaxExperts];
   __shared__ int wave_tot[3][16];
   __shared__ uint32_t slotmap_words[kSmallSlotBytes / 4];
+  __shared__ float wts_lds[kSmallPairs];
   uint8_t* slotmap = reinterpret_cast<uint8_t*>(slotmap_words);
   const int T = p.T, E = p.E, k = p.k;
   const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id();
@@ -228,6 +240,7 @@ __global__ __launch_bounds__(1024) void route_small_kernel(RouteParams p) {
     if (lane < k) {
       p.ids[t * k + lane] = id;
       p.wts[t * k + lane] = w;
+      wts_lds[t * k + lane] = w;
       atomicAdd(&counts[id], 1);
       slotmap[id * tpad + t] = static_cast<uint8_t>(lane + 1);
     }
@@ -263,7 +276,7 @@ __global__ __launch_bounds__(1024) void route_small_kernel(RouteParams p) {
     if (cnt > 0) {
       p.hit[hit_idx] = tid;
       p.pass_start[hit_idx] = pass0;
-      write_slot(p.slot_table, p.pass_slot, hit_idx, tid, off, cnt, pass0, p.rows_per_pass);
+      write_slot(p.slot_table, p.pass_slot, p.pass_table, hit_idx, tid, off, cnt, pass0, p.rows_per_pass);
     }
     if (tid == E - 1) {
       const int nh = hit_idx + (cnt > 0 ? 1 : 0);
@@ -271,7 +284,7 @@ __global__ __launch_bounds__(1024) void route_small_kernel(RouteParams p) {
       p.offsets[E] = off + cnt;
       p.pass_start[nh] = total;
       if (p.has_shared) {
-        write_slot(p.slot_table, p.pass_slot, nh, -1, 0, T, total, p.rows_per_pass);
+        write_slot(p.slot_table, p.pass_slot, p.pass_table, nh, -1, 0, T, total, p.rows_per_pass);
         total += passes_for(T, p.rows_per_pass);
       }
       p.pass_start[nh + p.has_shared] = total;
@@ -290,6 +303,8 @@ __global__ __launch_bounds__(1024) void route_small_kernel(RouteParams p) {
         const int flat = (q * 4 + byte) * k + static_cast<int>((word >> (byte * 8)) & 0xFFu) - 1;
         p.perm[pos] = flat;
         p.inv[flat] = pos;
+        p.slot_w[pos] = wts_lds[flat];
+        p.tok[pos] = q * 4 + byte;
         ++pos;
         word &= ~(0xFFu << (byte * 8));
       }
@@ -343,7 +358,7 @@ __global__ __launch_bounds__(256) void route_permute_kernel(RouteParams p) {
     if (cnt > 0) {
       p.hit[nz_before] = e;
       p.pass_start[nz_before] = pass_before;
-      write_slot(p.slot_table, p.pass_slot, nz_before, e, before, cnt, pass_before, p.rows_per_pass);
+      write_slot(p.slot_table, p.pass_slot, p.pass_table, nz_before, e, before, cnt, pass_before, p.rows_per_pass);
     }
     if (e == p.E - 1) {
       const int nh = nz_before + (cnt > 0 ? 1 : 0);
@@ -351,7 +366,7 @@ __global__ __launch_bounds__(256) void route_permute_kernel(RouteParams p) {
       p.offsets[p.E] = before + cnt;
       p.pass_start[nh] = total;
       if (p.has_shared) {
-        write_slot(p.slot_table, p.pass_slot, nh, -1, 0, p.T, total, p.rows_per_pass);
+        write_slot(p.slot_table, p.pass_slot, p.pass_table, nh, -1, 0, p.T, total, p.rows_per_pass);
         total += passes_for(p.T, p.rows_per_pass);
       }
       p.pass_start[nh + p.has_shared] = total;
@@ -371,6 +386,8 @@ __global__ __launch_bounds__(256) void route_permute_kernel(RouteParams p) {
       const int flat = t * p.k + slot1 - 1;
       p.perm[pos] = flat;
       p.inv[flat] = pos;
+      p.slot_w[pos] = p.wts[flat];
+      p.tok[pos] = t;
     }
     running += __popcll(mask);
   }
@@ -420,16 +437,21 @@ __global__ __launch_bounds__(512) void table_prep_kernel(TableParams p) {
     if (cnt[j] > 0) {
       p.hit[h] = e;
       p.pass_start[h] = ps;
-      write_slot(p.slot_table, p.pass_slot, h, e, p.offsets[e], cnt[j], ps, p.rows_per_pass);
+      write_slot(p.slot_table, p.pass_slot, p.pass_table, h, e, p.offsets[e], cnt[j], ps, p.rows_per_pass);
       ++h;
     }
     ps += passes_for(cnt[j], p.rows_per_pass);
+  }
+  for (int i = tid; i < p.T * p.k; i += 512) {
+    const int flat = p.perm[i];
+    p.slot_w[i] = p.wts[flat];
+    p.tok[i] = flat / p.k;
   }
   if (tid == 511) {
     int total = ps;
     p.pass_start[h] = total;
     if (p.has_shared) {
-      write_slot(p.slot_table, p.pass_slot, h, -1, 0, p.T, total, p.rows_per_pass);
+      write_slot(p.slot_table, p.pass_slot, p.pass_table, h, -1, 0, p.T, total, p.rows_per_pass);
       total += passes_for(p.T, p.rows_per_pass);
     }
     p.pass_start[h + p.has_shared] = total;
@@ -440,19 +462,33 @@ __global__ __launch_bounds__(512) void table_prep_kernel(TableParams p) {
 
 // ---------------------------------------------------------------------------
 // Combine: out[t] = sum_slot y[inv[t*k+slot]] (+ y[T*k + t] for the shared
-// expert), fp32 in slot order, one bf16 rounding.  grid = T, block = 256.
-__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y, const int32_t* __restrict__ inv, int T,
-                                                      int k, int H, int has_shared, uint16_t* __restrict__ out) {
+// expert), fp32 in slot order, one bf16 rounding.  grid = (T, H / 512),
+// block = 64: a lane owns 8 columns; the rows are read 8 at a time, all loads
+// of a batch in flight together, and added in slot order.
+__global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ y, const int32_t* __restrict__ inv, int T,
+                                                     int k, int H, int has_shared, uint16_t* __restrict__ out) {
   const int t = blockIdx.x;
+  const int c = (blockIdx.y * 64 + threadIdx.x) * 8;
   const int nrows = k + (has_shared ? 1 : 0);
-  for (int c = threadIdx.x * 8; c < H; c += 256 * 8) {
+  if (c < H) {
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < nrows; ++s) {
-      const int64_t row = s < k ? inv[t * k + s] : static_cast<int64_t>(T) * k + t;
-      const float4* src = reinterpret_cast<const float4*>(y + row * H + c);
-      const float4 a = src[0], b = src[1];
-      acc[0] += a.x; acc[1] += a.y; acc[2] += a.z; acc[3] += a.w;
-      acc[4] += b.x; acc[5] += b.y; acc[6] += b.z; acc[7] += b.w;
+    for (int s0 = 0; s0 < nrows; s0 += 8) {
+      float4 a[8], b[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int s = min(s0 + i, nrows - 1);
+        const int64_t row = s < k ? ld_const(inv, t * k + s) : static_cast<int64_t>(T) * k + t;
+        const float4* src = reinterpret_cast<const float4*>(y + row * H + c);
+        a[i] = src[0];
+        b[i] = src[1];
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (s0 + i < nrows) {
+          acc[0] += a[i].x; acc[1] += a[i].y; acc[2] += a[i].z; acc[3] += a[i].w;
+          acc[4] += b[i].x; acc[5] += b[i].y; acc[6] += b[i].z; acc[7] += b[i].w;
+        }
+      }
     }
     uint4 o;
     o.x = f32_to_bf16(acc[0]) | (static_cast<uint32_t>(f32_to_bf16(acc[1])) << 16);
@@ -502,7 +538,7 @@ void launch_table_prep(const TableParams& p, hipStream_t stream) {
 void launch_combine(const float* y, const int32_t* inv, int T, int k, int H, int has_shared, uint16_t* out,
                     hipStream_t stream) {
   if (T <= 0) return;
-  hipLaunchKernelGGL(combine_kernel, dim3(T), dim3(256), 0, stream, y, inv, T, k, H, has_shared, out);
+  hipLaunchKernelGGL(combine_kernel, dim3(T, (H + 511) / 512), dim3(64), 0, stream, y, inv, T, k, H, has_shared, out);
 }
 
 }  // namespace dflash

@@ -31,7 +31,7 @@ __device__ __forceinline__ void w4_pass(const W4StreamParams& p, const uint8_t* 
 #pragma unroll
   for (int mt = 0; mt < kMT; ++mt) {
     const int m = min(m0 + mt * 16 + lr, M - 1);
-    if (kMode == kModeGateUp) arow[mt] = shared ? m : p.perm[seg + m] / p.top_k;
+    if (kMode == kModeGateUp) arow[mt] = shared ? m : p.tok[seg + m];
     else if (kMode == kModeDown) arow[mt] = shared ? p.T * p.top_k + m : seg + m;
     else arow[mt] = m;
   }
@@ -135,7 +135,7 @@ __device__ __forceinline__ void w4_pass(const W4StreamParams& p, const uint8_t* 
         if (valid && lr == 0) p.out_part[static_cast<int64_t>(hrow) * (inter >> 4) + strip] = -kDequantOffset * part;
       } else {
         if (valid) {
-          const float wgt = shared ? p.shared_gate[m] : p.route_w[p.perm[seg + m]];
+          const float wgt = shared ? p.shared_gate[m] : p.slot_w[seg + m];
           const int yrow = shared ? p.T * p.top_k + m : seg + m;
           float* o = p.out_f32 + static_cast<int64_t>(yrow) * p.N;
           o[row0 + lr] = tot0[mt][e] * wgt;
@@ -162,20 +162,17 @@ __global__ __launch_bounds__(256) void w4_gemm_kernel(W4StreamParams p, int max_
     s = static_cast<const ScaleT*>(p.s);
     M = p.M;
   } else {
-    const int nh = p.meta[0];
-    if (slot < nh) {
-      const int e = p.hit[slot];
-      seg = p.offsets[e];
-      M = p.offsets[e + 1] - seg;
-      w = p.w + e * p.w_stride;
-      s = static_cast<const ScaleT*>(p.s) + e * p.s_stride;
-    } else if (slot == nh && p.has_shared) {
+    if (slot >= p.meta[0] + p.has_shared) return;
+    const int4 d = p.slot_table[slot];  // expert (-1 shared), segment start, rows, first pass
+    seg = d.y;
+    M = d.z;
+    if (d.x < 0) {
       shared = true;
-      M = p.T;
       w = p.w_shared;
       s = static_cast<const ScaleT*>(p.s_shared);
     } else {
-      return;
+      w = p.w + d.x * p.w_stride;
+      s = static_cast<const ScaleT*>(p.s) + d.x * p.s_stride;
     }
   }
   int row0, row1;

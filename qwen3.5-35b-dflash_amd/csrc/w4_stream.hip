@@ -20,9 +20,9 @@
 // MFMAs.  Every weight or scale address is a lane-constant 32-bit offset,
 // computed once, on top of a wave-uniform base that the scalar unit advances
 // (the global_load saddr form); a slot descriptor is one s_load_dwordx4 per
-// slot change.  Weights are prefetched two units ahead through three register
-// buffers, issued unconditionally (clamped to the last unit of the range) so
-// the in-order vmcnt accounting keeps both newer buffers in flight.
+// slot change.  Weights are prefetched kDepth-1 units ahead through kDepth
+// register buffers, issued unconditionally (clamped to the last unit of the
+// range) so the in-order vmcnt accounting keeps all newer buffers in flight.
 //
 // Modes:
 //   kModeLinear : y = x . dequant(W)^T, bf16 out                 (fused/quantization.py:154-165)
@@ -101,10 +101,10 @@ __device__ __forceinline__ SlotDesc load_slot(const W4StreamParams& p, int slot,
   return d;
 }
 
-// Activation row of slot row m (pv = perm entry of that row).
+// Activation row of slot row m (tv = token of that row for gate/up).
 template <int kMode>
-__device__ __forceinline__ int act_row(const W4StreamParams& p, const SlotDesc& sd, int pv, int m) {
-  if (kMode == kModeGateUp) return sd.e < 0 ? m : pv / p.top_k;
+__device__ __forceinline__ int act_row(const W4StreamParams& p, const SlotDesc& sd, int tv, int m) {
+  if (kMode == kModeGateUp) return sd.e < 0 ? m : tv;
   if (kMode == kModeDown) return sd.e < 0 ? p.T * p.top_k + m : sd.seg + m;
   return m;
 }
@@ -117,20 +117,22 @@ __device__ __forceinline__ void load_act(ActRegs<kMT, kKBPW>& A, const W4StreamP
   const int K = p.K, nkb = K >> 7;
   constexpr int kParts = kMode == kModeDown ? 8 : 1;  // h: 8 partials of 16 columns per block; x: 1
   const bool shared = sd.e < 0;
-  int pa[kMT], pd[kMT][4];
+  int ta[kMT], td[kMT][4];
+  float wd[kMT][4];
 #pragma unroll
   for (int mt = 0; mt < kMT; ++mt) {
     const int m = min(m0 + mt * 16 + lr, sd.M - 1);
-    pa[mt] = kMode == kModeGateUp ? p.perm[shared ? 0 : sd.seg + m] : 0;
+    ta[mt] = kMode == kModeGateUp ? p.tok[shared ? 0 : sd.seg + m] : 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int md = min(m0 + mt * 16 + 4 * kq + e, sd.M - 1);
-      pd[mt][e] = kMode != kModeLinear ? p.perm[shared ? 0 : sd.seg + md] : 0;
+      td[mt][e] = kMode == kModeGateUp ? p.tok[shared ? 0 : sd.seg + md] : 0;
+      wd[mt][e] = kMode == kModeDown ? (shared ? p.shared_gate[md] : p.slot_w[sd.seg + md]) : 0.f;
     }
   }
 #pragma unroll
   for (int mt = 0; mt < kMT; ++mt) {
-    const int arow = act_row<kMode>(p, sd, pa[mt], min(m0 + mt * 16 + lr, sd.M - 1));
+    const int arow = act_row<kMode>(p, sd, ta[mt], min(m0 + mt * 16 + lr, sd.M - 1));
     const uint16_t* ap = p.act + static_cast<int64_t>(arow) * K + ks * kKBPW * 128 + kq * 32;
 #pragma unroll
     for (int kb = 0; kb < kKBPW; ++kb)
@@ -139,7 +141,7 @@ __device__ __forceinline__ void load_act(ActRegs<kMT, kKBPW>& A, const W4StreamP
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int md = min(m0 + mt * 16 + 4 * kq + e, sd.M - 1);
-      const int drow = act_row<kMode>(p, sd, pd[mt][e], md);
+      const int drow = act_row<kMode>(p, sd, td[mt][e], md);
       const float* np = p.act_neg + static_cast<int64_t>(drow) * nkb * kParts + ks * kKBPW * kParts;
 #pragma unroll
       for (int kb = 0; kb < kKBPW; ++kb) {
@@ -148,7 +150,7 @@ __device__ __forceinline__ void load_act(ActRegs<kMT, kKBPW>& A, const W4StreamP
         for (int c = 0; c < kParts; ++c) v += np[kb * kParts + c];
         A.xn[mt][kb][e] = v;
       }
-      if (kMode == kModeDown) A.wgt[mt][e] = (shared ? p.shared_gate : p.route_w)[shared ? md : pd[mt][e]];
+      if (kMode == kModeDown) A.wgt[mt][e] = wd[mt][e];
     }
   }
 }
@@ -197,6 +199,12 @@ __device__ __forceinline__ void compute_unit(const WeightBuf<kKBPW, ScaleT>& b, 
   }
 }
 
+// Register buffers in the weight pipeline.  A unit holds 2*kKBPW 16-byte
+// loads per lane; deeper pipelines keep more bytes in flight per CU, bounded
+// by the VGPR budget of two waves per SIMD (the activations of kMT token
+// tiles take the rest).
+constexpr int stream_depth(int kbpw, int) { return kbpw == 1 ? 4 : 3; }
+
 }  // namespace
 
 template <int kMode, int kMT, int kKBPW, typename ScaleT>
@@ -214,6 +222,8 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(W4StreamParams p) {
   const int u_begin = static_cast<int>(total_units * blockIdx.x / gridDim.x);
   const int u_end = static_cast<int>(total_units * (blockIdx.x + 1) / gridDim.x);
   if (u_begin >= u_end) return;
+  // units in flight: kDepth - 1 prefetched while one is computed
+  constexpr int kDepth = stream_depth(kKBPW, kMT);
 
   // ---- geometry: lane-constant 32-bit offsets, uniform strides
   const int64_t rb = p.K >> 1;  // packed bytes per weight row
@@ -266,9 +276,9 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(W4StreamParams p) {
     }
   };
 
-  WeightBuf<kKBPW, ScaleT> b0, b1, b2;
-  issue(b0);
-  issue(b1);
+  WeightBuf<kKBPW, ScaleT> wb[kDepth];
+#pragma unroll
+  for (int i = 0; i + 1 < kDepth; ++i) issue(wb[i]);
 
   // ---- compute stream
   int c_P = u_begin / p.strips, c_strip = u_begin - c_P * p.strips;
@@ -344,10 +354,9 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(W4StreamParams p) {
     buf ^= 1;
   };
 
-  for (int u = u_begin; u < u_end; u += 3) {
-    step(u, b0, b2);
-    step(u + 1, b1, b0);
-    step(u + 2, b2, b1);
+  for (int u = u_begin; u < u_end; u += kDepth) {
+#pragma unroll
+    for (int i = 0; i < kDepth; ++i) step(u + i, wb[i], wb[(i + kDepth - 1) % kDepth]);
   }
 }
 

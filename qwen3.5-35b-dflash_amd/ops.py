@@ -222,3 +222,16 @@ def moe_workspace_bytes(tokens: int, hidden: int, inter: int, experts: int, top_
                         has_shared: bool) -> int:
     return int(_lib.load().dflash_moe_workspace_bytes(tokens, hidden, inter, experts, top_k, group_size,
                                                       int(has_shared)))
+
+
+STAGE_GATE_UP = _lib.STAGE_GATE_UP
+STAGE_DOWN = _lib.STAGE_DOWN
+
+
+def set_measure_stage(stage: int) -> None:
+    """Measurement mode: later MoE calls launch only ``stage``'s kernel (0 restores full calls).
+
+    The kernel reuses what an earlier full call with the same arguments left
+    in the same workspace; the layer output is not written.
+    """
+    _lib.call("dflash_set_measure_stage", int(stage))

@@ -89,6 +89,9 @@ def test_moe_prefill_t2048(pkg, device):
     (40, 4, 1, 1024, 512, 256, torch.bfloat16, True),
     (37, 16, 4, 512, 1024, 128, torch.float32, True),
     (70, 4, 4, 512, 512, 128, torch.bfloat16, True),          # E == k: every token hits every expert
+    (20, 16, 4, 1024, 1024, 128, torch.float32, True),        # small-T kernel: K = 1024 both ways, fp32 scales
+    (32, 64, 8, 2048, 512, 128, torch.bfloat16, True),        # small-T kernel at its largest T
+    (9, 8, 8, 512, 512, 128, torch.bfloat16, True),           # small-T kernel, E == k
 ])
 def test_moe_small_shapes(pkg, device, tokens, experts, k, hidden, inter, group, scale_dtype, shared):
     print(f"moe T={tokens} E={experts} k={k} H={hidden} I={inter} g={group} {scale_dtype} shared={shared}",
@@ -135,3 +138,24 @@ def test_moe_repeat_calls_are_identical(pkg, device):
     a = pkg.ops.moe_w4a16(x, gu, dn, top_k=8, router_weight=rw, shared=sh)
     b = pkg.ops.moe_w4a16(x, gu, dn, top_k=8, router_weight=rw, shared=sh)
     assert torch.equal(a, b)
+
+
+def test_measure_stage_relaunches_one_kernel(pkg, device):
+    """Measurement mode re-runs one stage on the workspace of a full call and rewrites identical bytes."""
+    layer = pkg.synthetic.moe_layer(16, seed=6)
+    gu, dn, sh = _to(pkg, layer, device)
+    x, rw = layer.hidden.to(device), layer.router_weight.to(device)
+    ws = torch.empty(pkg.ops.moe_workspace_bytes(16, 2048, 512, 256, 8, 128, True), dtype=torch.uint8, device=device)
+    ref = pkg.ops.moe_w4a16(x, gu, dn, top_k=8, router_weight=rw, shared=sh, workspace=ws)
+    torch.cuda.synchronize()
+    snapshot = ws.clone()
+    for stage in (pkg.ops.STAGE_GATE_UP, pkg.ops.STAGE_DOWN):
+        pkg.ops.set_measure_stage(stage)
+        try:
+            pkg.ops.moe_w4a16(x, gu, dn, top_k=8, router_weight=rw, shared=sh, workspace=ws)
+        finally:
+            pkg.ops.set_measure_stage(0)
+        torch.cuda.synchronize()
+        assert torch.equal(ws, snapshot), stage
+    again = pkg.ops.moe_w4a16(x, gu, dn, top_k=8, router_weight=rw, shared=sh, workspace=ws)
+    assert torch.equal(again, ref)

@@ -29,6 +29,8 @@ def _case(pkg, m, n, k, group, scale_dtype, seed):
     (33, 64, 4096, 256, torch.bfloat16),
     (64, 96, 1024, 128, torch.float32),
     (16, 2048, 512, 128, torch.bfloat16),
+    (32, 64, 1024, 128, torch.float32),
+    (24, 128, 2048, 128, torch.float32),
 ])
 def test_qlinear_matches_oracle(pkg, device, m, n, k, group, scale_dtype):
     print(f"qlinear m={m} n={n} k={k} g={group} {scale_dtype}", flush=True)

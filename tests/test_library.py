@@ -145,3 +145,10 @@ def test_python_wrappers_refuse_cpu_tensors(pkg):
         pkg.ops.qlinear(x, w)
     with pytest.raises(ValueError, match="ROCm device"):
         pkg.ops.route(torch.zeros((4, 16)), 2)
+
+
+def test_measure_stage_validation(pkg):
+    lib = pkg._lib.load()
+    assert lib.dflash_set_measure_stage(7) == 1
+    assert "stage" in lib.dflash_last_error().decode()
+    assert lib.dflash_set_measure_stage(0) == 0
