@@ -150,7 +150,21 @@ bool moe_wave_path(const MoeShapes& S) {
          w4_wave_supports(kModeDown, static_cast<int>(S.I), 128, 0);
 }
 
-int rows_per_pass(const MoeShapes& S) { return moe_wave_path(S) ? 16 : 16 * token_tiles(S.T); }
+// Long prefill (at least 16 rows per expert on average) runs both expert GEMMs
+// on the LDS-tiled kernel, whose passes hold 96 rows.
+bool moe_tile_path(const MoeShapes& S) {
+  using namespace dflash;
+  const int64_t rows = S.T * S.k + S.T;
+  return !moe_wave_path(S) && S.T * S.k >= 16 * S.E && rows * std::max(S.H, S.I) < (int64_t(1) << 31) &&
+         w4_tile_supports(kModeGateUp, static_cast<int>(2 * S.I), static_cast<int>(S.H), static_cast<int>(S.G)) &&
+         w4_tile_supports(kModeDown, static_cast<int>(S.H), static_cast<int>(S.I), static_cast<int>(S.Gd));
+}
+
+int rows_per_pass(const MoeShapes& S) {
+  if (moe_wave_path(S)) return 16;
+  if (moe_tile_path(S)) return dflash::kTileRowsPerPass;
+  return 16 * token_tiles(S.T);
+}
 
 int check_moe(const void* hidden, int64_t T, int64_t H, int64_t k, const dflash_w4* gate_up, const dflash_w4* down,
               const dflash_w4* sgu, const dflash_w4* sdn, const void* sgate, const void* out, MoeShapes* S) {
@@ -196,11 +210,18 @@ bool stage_on(int stage) {
 // One W4 GEMM over the work table: the wave-streaming kernel for small T
 // (wave == true), else the workgroup-streaming kernel when it splits this K
 // evenly, else the per-wave fallback.
-void launch_w4(int mode, bool fp32_scales, int mt, int max_slots, bool wave, dflash::W4StreamParams& p,
+enum class GemmPath { kWave, kTile, kStream };
+
+void launch_w4(int mode, bool fp32_scales, int mt, int max_slots, GemmPath path, dflash::W4StreamParams& p,
                hipStream_t stream) {
   using namespace dflash;
+  if (path == GemmPath::kTile) {
+    p.strips = mode == kModeGateUp ? p.N / 2 / 256 : p.N / 512;  // column tiles per pass
+    launch_w4_tile(mode, fp32_scales, cu_count(), p, stream);
+    return;
+  }
   const int cols = mode == kModeGateUp ? p.N / 2 / 16 : p.N / 32;  // 16-column pairs or 32-row strips
-  if (wave) {
+  if (path == GemmPath::kWave) {
     p.strips = cols;
     launch_w4_wave(mode, fp32_scales, cu_count(), p, stream);
     return;
@@ -222,8 +243,8 @@ int run_experts(const MoeShapes& S, const int32_t* inv, void* ws, const MoeLayou
   using namespace dflash;
   const int T = static_cast<int>(S.T), H = static_cast<int>(S.H), I = static_cast<int>(S.I);
   const int k = static_cast<int>(S.k);
-  const bool wave = moe_wave_path(S);
-  const int mt = wave ? 1 : token_tiles(S.T);
+  const GemmPath path = moe_wave_path(S) ? GemmPath::kWave : moe_tile_path(S) ? GemmPath::kTile : GemmPath::kStream;
+  const int mt = path == GemmPath::kStream ? token_tiles(S.T) : 1;
   const int32_t* meta = at<int32_t>(ws, L.route.meta);
   const int4* slot_table = at<int4>(ws, L.route.slot_table);
   const int32_t* pass_slot = at<int32_t>(ws, L.route.pass_slot);
@@ -236,7 +257,7 @@ int run_experts(const MoeShapes& S, const int32_t* inv, void* ws, const MoeLayou
   p.top_k = k;
   p.T = T;
   p.has_shared = S.shared ? 1 : 0;
-  p.rows_per_pass = 16 * mt;
+  p.rows_per_pass = rows_per_pass(S);
   const int max_slots = static_cast<int>(std::min<int64_t>(S.E, S.T * S.k)) + p.has_shared;
 
   // gate_up: N = 2I rows over K = H, SiLU*up epilogue into h
@@ -254,7 +275,7 @@ int run_experts(const MoeShapes& S, const int32_t* inv, void* ws, const MoeLayou
   p.neg_parts = 1;
   p.out_bf16 = at<uint16_t>(ws, L.h);
   p.out_part = at<float>(ws, L.hpart);
-  if (stage_on(DFLASH_STAGE_GATE_UP)) launch_w4(kModeGateUp, S.gu_f32, mt, max_slots, wave, p, stream);
+  if (stage_on(DFLASH_STAGE_GATE_UP)) launch_w4(kModeGateUp, S.gu_f32, mt, max_slots, path, p, stream);
   if (int r = launch_status("gate_up")) return r;
 
   // down: N = H rows over K = I, routing-weight epilogue into y
@@ -269,13 +290,13 @@ int run_experts(const MoeShapes& S, const int32_t* inv, void* ws, const MoeLayou
   p.G = static_cast<int>(down->group_size);
   p.act = at<uint16_t>(ws, L.h);
   p.act_neg = at<float>(ws, L.hpart);
-  p.neg_parts = 8;
+  p.neg_parts = path == GemmPath::kTile ? 1 : 8;  // the tile kernel's gate_up sums h per 128 columns
   p.out_bf16 = nullptr;
   p.out_part = nullptr;
   p.out_f32 = at<float>(ws, L.y);
   p.slot_w = at<float>(ws, L.route.slot_w);
   p.shared_gate = at<float>(ws, L.gate);
-  if (stage_on(DFLASH_STAGE_DOWN)) launch_w4(kModeDown, S.dn_f32, mt, max_slots, wave, p, stream);
+  if (stage_on(DFLASH_STAGE_DOWN)) launch_w4(kModeDown, S.dn_f32, mt, max_slots, path, p, stream);
   if (int r = launch_status("down")) return r;
 
   if (measuring()) return DFLASH_OK;
@@ -370,7 +391,8 @@ int dflash_qlinear_w4a16(const void* x, int64_t m, const dflash_w4* weight, void
                       dflash::w4_wave_supports(dflash::kModeLinear, p.K, p.G, static_cast<int>(m));
     const int mt = wave ? 1 : token_tiles(m);
     p.rows_per_pass = 16 * mt;
-    launch_w4(dflash::kModeLinear, weight->scale_dtype == DFLASH_DTYPE_F32, mt, 1, wave, p, st);
+    launch_w4(dflash::kModeLinear, weight->scale_dtype == DFLASH_DTYPE_F32, mt, 1, wave ? GemmPath::kWave : GemmPath::kStream,
+              p, st);
     return launch_status("qlinear");
   } catch (...) {
     return fail(DFLASH_ERR_HIP, "unexpected host exception");

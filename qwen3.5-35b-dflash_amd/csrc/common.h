@@ -53,6 +53,23 @@ __device__ __forceinline__ int4 ld_const_int4(const int4* p, int i) {
   return make_int4(v.x, v.y, v.z, v.w);
 }
 
+// Raw buffer resource over [base, base + bytes): loads through it take a 32-bit
+// VGPR byte offset plus a wave-uniform SGPR offset, and read 0 past the end.
+typedef __amdgpu_buffer_rsrc_t buf_rsrc;
+constexpr int kBufferDword3 = 0x00020000;  // 32-bit data format, raw (stride 0) addressing
+
+__device__ __forceinline__ buf_rsrc make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                           kBufferDword3);
+}
+__device__ __forceinline__ uint4 buf_load16(buf_rsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voff),
+                                                                         static_cast<int>(soff), 0));
+}
+__device__ __forceinline__ float buf_load_f32(buf_rsrc r, uint32_t voff, uint32_t soff) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(voff), static_cast<int>(soff), 0));
+}
+
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bits) {
   uint32_t d;
   // gfx9 VOP3 reads at most one SGPR: mask from an SGPR, the magic bits from a VGPR.
@@ -85,12 +102,9 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t v) {
   return __uint_as_float(static_cast<uint32_t>(v) << 16);
 }
 
-// Round-to-nearest-even fp32 -> bf16 (NaN stays NaN).
+// Round-to-nearest-even fp32 -> bf16 (NaN stays NaN): one v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 // Raw scale bits (no conversion at load time, so a prefetched scale does not
@@ -130,6 +144,7 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+// g * sigmoid(g); the product is rounded to bf16 afterwards, so the 1-ulp reciprocal suffices.
+__device__ __forceinline__ float silu(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 
 }  // namespace dflash

@@ -117,7 +117,7 @@ struct W4StreamParams {
   int strips;              // units per pass
   // outputs
   uint16_t* out_bf16;      // kModeLinear: [M][N]; kModeGateUp: h [(T*k+T)][N/2] interleaved
-  float* out_part;         // kModeGateUp: [(T*k+T)][N/32] partial -136*sum(h) per 16 columns
+  float* out_part;         // kModeGateUp: [(T*k+T)][N/32] partial -136*sum(h) per 16 columns ([N/256] per 128 on the tile kernel)
   float* out_f32;          // kModeDown: y [(T*k+T)][N]
   const float* slot_w;     // kModeDown: routing weight of every slot row [T*k]
   const float* shared_gate;// kModeDown: sigmoid gate [T]
@@ -144,5 +144,11 @@ void launch_w4_stream(int mode, bool fp32_scales, int mt, int grid, const W4Stre
 bool w4_wave_supports(int mode, int K, int G, int rows);
 constexpr int kWaveMaxTokenRows = 2048;  // T * top_k routed slot rows whose tokens stay in LDS
 void launch_w4_wave(int mode, bool fp32_scales, int grid, const W4StreamParams& p, hipStream_t stream);
+// LDS-tiled kernel for long prefill (w4_tile.hip): 96-row passes, column tiles of 512
+// (p.strips = I / 256 for gate_up, H / 512 for down), K % 512 == 0; its gate_up writes one
+// -136*sum(h) per 128 columns and its down reads them that way.
+constexpr int kTileRowsPerPass = 96;
+bool w4_tile_supports(int mode, int N, int K, int G);
+void launch_w4_tile(int mode, bool fp32_scales, int grid, const W4StreamParams& p, hipStream_t stream);
 
 }  // namespace dflash

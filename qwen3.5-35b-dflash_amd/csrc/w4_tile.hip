@@ -1,0 +1,374 @@
+// LDS-tiled grouped W4A16 GEMM for long prefill (many rows per expert).
+//
+// A work tile is one pass (up to 96 rows of one slot: an expert segment or
+// the shared expert) times one column tile of 512 outputs; persistent
+// workgroups (one per CU, 8 waves, 64 columns each) take tiles round robin.
+// Per 128-column k-block of the reduction:
+//   * every operand reaches LDS by direct-to-LDS buffer loads (no register
+//     staging): the pass's activation rows in MFMA fragment order (1 KB
+//     blocks, one per 16-row subtile and 32-k step) and their -136*sum terms,
+//     two stages, one k-block ahead; each wave's own weight fragments (16
+//     columns x 128 k, 16 bytes per lane) and their group scales, three
+//     stages, two k-blocks ahead.  Every stage is its own LDS array, so the
+//     compiler waits only for the loads that filled the array it reads.
+//     One barrier per k-block publishes the activation stage.
+//   * the weights are dequantised once per wave to bf16 (136 + q), exact, with
+//     8 VALU operations per 8 weights, and each dequantised word feeds one
+//     v_mfma_f32_16x16x32_bf16 per 16-row subtile;
+//   * the MFMAs accumulate straight into u = sum_kb' s_kb' acc_kb' / s_kb, the
+//     running sum in units of the current group scale: at each k-block u is
+//     rescaled by s_prev / s_kb and offset by -136*sum(a) in one FMA, so no
+//     per-k-block accumulator set is held; the tile ends with tot = u * s_last.
+//     Group scales are clamped to |s| >= 2^-64 (a zero group adds nothing
+//     either way) so the ratios stay finite.
+// The k-loop is specialised on the pass's subtile count, so a k-step is one
+// straight-line block: while its MFMAs run the wave refills each subtile's A
+// fragment for the next k-step right after the subtile's last MFMA and
+// dequantises the next k-step's weights; the last k-step also reads and
+// dequantises the next k-block's weights.
+//
+// Modes (reference citations):
+//   kModeGateUp : h = silu(x.Wg^T) * (x.Wu^T), bf16, octet-interleaved, and its
+//                 -136*sum per 128 columns for the down GEMM        (reference/fused_ops.py:170-171)
+//   kModeDown   : y = route_weight * (h . Wd^T), fp32              (fused/quantization.py:196-199)
+#include <type_traits>
+
+#include "kernels.h"
+
+namespace dflash {
+namespace {
+
+constexpr int kTileM = 96;                  // rows per pass (6 subtiles of 16)
+constexpr int kMaxSub = kTileM / 16;
+constexpr int kWaves = 8;
+constexpr int kTileN = kWaves * 64;         // output columns per tile
+constexpr int kBlocks = kMaxSub * 4;        // activation fragment blocks per stage (subtile x k-step), 1 KB each
+constexpr int kAStages = 2, kWStages = 3;
+
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+template <int N>
+using Idx = std::integral_constant<int, N>;
+
+// The stages, each a separate __shared__ array of the kernel.
+struct TileLds {
+  uint4* a[kAStages];       // [kBlocks][64 lanes] activation fragments
+  float* neg[kAStages];     // [128] -136*sum of each row's k-block (rows past the pass repeat the last)
+  uint4* w[kWStages];       // [kWaves][4 fragments][64 lanes] packed weights
+  uint32_t* s[kWStages];    // [kWaves][4 fragments x 16 columns] raw scale bits
+};
+
+// Per-tile state shared by the subtile-count specialisations.
+struct TileCtx {
+  int4 d;                   // expert (-1 shared), segment start, slot rows, first row of the pass
+  bool shared;
+  int rows, nt;
+  buf_rsrc wrs, srs, ars, nrs;  // the slot's weights and scales, activations, their -136*sum terms
+  uint32_t woff[4];         // byte offset of this lane's 16 bytes of each weight fragment (k-block 0)
+  uint32_t soff;            // byte offset of the scale row this lane loads (fragment lane >> 4, column lane & 15)
+  uint32_t aoff[3];         // byte offset of this lane's 16 bytes of activation blocks wave, wave + 8, wave + 16
+  uint32_t noff;            // byte offset of the -136*sum terms of row 64 * wave + lane
+};
+
+__device__ __forceinline__ void dma16(buf_rsrc r, void* dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)dst, 16, static_cast<int>(voff), static_cast<int>(soff), 0, 0);
+}
+__device__ __forceinline__ void dma4(buf_rsrc r, void* dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)dst, 4, static_cast<int>(voff), static_cast<int>(soff), 0, 0);
+}
+
+// Workgroup barrier publishing this wave's direct-to-LDS loads older than its
+// newest kPending ones.  __syncthreads() would not do: its release fence counts
+// every load still headed for LDS as a pending LDS write and waits for all of
+// them.  The empty asm statements keep the compiler from moving memory
+// accesses across the barrier.
+template <int kPending>
+__device__ __forceinline__ void dma_barrier() {
+  static_assert(kPending < 16, "vmcnt field");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0070 | kPending);  // vmcnt(kPending) lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// scheduling-group masks of __builtin_amdgcn_sched_group_barrier
+constexpr int kSchedValu = 0x002, kSchedMfma = 0x008, kSchedDsRead = 0x100;
+
+// Instruction order of one k-step's scheduling region: kLead VALU operations,
+// then kMfma x (1 MFMA, kValu VALU operations), with one LDS read after every
+// kDsEvery MFMAs, so the VALU work issues while the MFMAs run.
+template <int kLead, int kMfma, int kValu, int kDsEvery>
+__device__ __forceinline__ void interleave() {
+  if (kLead) __builtin_amdgcn_sched_group_barrier(kSchedValu, kLead, 0);
+#pragma unroll
+  for (int i = 0; i < kMfma; ++i) {
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedValu, kValu, 0);
+    if ((i + 1) % kDsEvery == 0) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+  }
+}
+
+template <int kMode, typename ScaleT, int NSUB>
+__device__ __forceinline__ void tile_pass(const W4StreamParams& p, const TileLds& lds, const TileCtx& c) {
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = lane_id(), lr = lane & 15, kq = lane >> 4;
+  const int nkb = p.K >> 7, gshift = p.G == 256 ? 1 : 0;
+  const int inter = p.N >> 1;
+
+  // loads of k-block kb (clamped: past the end they repeat the last k-block into a stage never read)
+  auto load_a = [&](int kb, auto sa) {
+    kb = min(kb, nkb - 1);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      const int b = wave + kWaves * i;
+      if (b < NSUB * 4) dma16(c.ars, lds.a[sa] + b * 64, c.aoff[i], kb * 256);
+    }
+    if (wave * 64 < NSUB * 16) dma4(c.nrs, lds.neg[sa] + wave * 64, c.noff, kb * 4);
+  };
+  auto load_w = [&](int kb, auto sw) {
+    kb = min(kb, nkb - 1);
+#pragma unroll
+    for (int f = 0; f < 4; ++f) dma16(c.wrs, lds.w[sw] + (wave * 4 + f) * 64, c.woff[f], kb * 64);
+    const int g = kb >> gshift;
+    dma4(c.srs, lds.s[sw] + wave * 64, c.soff, sizeof(ScaleT) == 4 ? g * 4 : (g & ~1) * 2);
+  };
+  // this lane's weights and group scales of k-block kb from stage sw
+  auto read_w = [&](uint4 (&wf)[4], float (&sc)[4], int kb, auto sw) {
+    const int g = kb >> gshift;
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      wf[f] = lds.w[sw][(wave * 4 + f) * 64 + lane];
+      const uint32_t bits = lds.s[sw][wave * 64 + f * 16 + lr];
+      float v = sizeof(ScaleT) == 4 ? __uint_as_float(bits) : __uint_as_float((g & 1 ? bits >> 16 : bits & 0xFFFFu) << 16);
+      if (__builtin_fabsf(v) < 0x1p-64f) v = __builtin_copysignf(0x1p-64f, v);  // NaN passes through
+      sc[f] = v;
+    }
+  };
+  auto word = [](const uint4& w, int j) { return j == 0 ? w.x : j == 1 ? w.y : j == 2 ? w.z : w.w; };
+
+  // prologue: weights of k-blocks 0 and 1, activations of k-block 0 (the empty asm statements keep
+  // the issue order the barrier's load count relies on)
+  load_w(0, Idx<0>{});
+  load_a(0, Idx<0>{});
+  asm volatile("" ::: "memory");
+  load_w(1, Idx<1>{});
+
+  f32x4 u[NSUB][4];  // running sums in units of the current k-block's scale
+  float s_prev[4] = {0.f, 0.f, 0.f, 0.f}, s_next[4];
+  uint4 wf[4];       // packed weights of the k-block about to run
+  uint4 bc[4];       // dequantised weights of the k-step about to run
+  uint4 a[NSUB];     // activation fragments of the k-step about to run
+#pragma unroll
+  for (int ms = 0; ms < NSUB; ++ms)
+#pragma unroll
+    for (int f = 0; f < 4; ++f) u[ms][f] = f32x4{0.f, 0.f, 0.f, 0.f};
+  read_w(wf, s_next, 0, Idx<0>{});
+#pragma unroll
+  for (int f = 0; f < 4; ++f) bc[f] = dequant8(wf[f].x);
+
+  auto step = [&](int kb, auto sa_tag, auto sw_tag) {
+    constexpr int sa = decltype(sa_tag)::value, sw = decltype(sw_tag)::value;
+    // the activation stage of k-block kb is complete once this wave's loads older than the
+    // last 5 (weights and scales of k-block kb + 1) are
+    dma_barrier<5>();
+    load_a(kb + 1, Idx<(sa + 1) % kAStages>{});
+    asm volatile("" ::: "memory");
+    load_w(kb + 2, Idx<(sw + 2) % kWStages>{});
+#pragma unroll
+    for (int ms = 0; ms < NSUB; ++ms) a[ms] = lds.a[sa][ms * 4 * 64 + lane];
+    // u <- u * s_prev / s_kb - 136 * sum(a_kb)   (k-block 0: u = -136 * sum)
+    float ratio[4];
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      ratio[f] = s_prev[f] * __builtin_amdgcn_rcpf(s_next[f]);
+      s_prev[f] = s_next[f];
+    }
+#pragma unroll
+    for (int ms = 0; ms < NSUB; ++ms) {
+      const f32x4 start = *reinterpret_cast<const f32x4*>(lds.neg[sa] + ms * 16 + 4 * kq);
+#pragma unroll
+      for (int f = 0; f < 4; ++f) u[ms][f] = u[ms][f] * ratio[f] + start;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int ms = 0; ms < NSUB; ++ms) {
+#pragma unroll
+        for (int f = 0; f < 4; ++f) u[ms][f] = mfma16x16x32(a[ms], bc[f], u[ms][f]);
+        if (j < 3) a[ms] = lds.a[sa][(ms * 4 + j + 1) * 64 + lane];
+      }
+      if (j == 3) read_w(wf, s_next, kb + 1, Idx<(sw + 1) % kWStages>{});
+#pragma unroll
+      for (int f = 0; f < 4; ++f) bc[f] = dequant8(word(wf[f], (j + 1) & 3));
+      // k-step 0 also holds the rescale (16 FMAs per subtile, the first subtile's ahead of all MFMAs),
+      // k-step 3 the next k-block's weight and scale reads
+      if (j == 0) interleave<24, 4 * NSUB, (16 * NSUB + 24) / (4 * NSUB), 2>();
+      else if (j == 3) interleave<0, 4 * NSUB, 3, 2>();
+      else interleave<0, 4 * NSUB, 2, 4>();
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  for (int kb = 0; kb < nkb; kb += 6) {  // nkb is even; stage indices repeat every 6 k-blocks
+    step(kb, Idx<0>{}, Idx<0>{});
+    step(kb + 1, Idx<1>{}, Idx<1>{});
+    if (kb + 2 < nkb) {
+      step(kb + 2, Idx<0>{}, Idx<2>{});
+      step(kb + 3, Idx<1>{}, Idx<0>{});
+    }
+    if (kb + 4 < nkb) {
+      step(kb + 4, Idx<0>{}, Idx<1>{});
+      step(kb + 5, Idx<1>{}, Idx<2>{});
+    }
+  }
+  // no load may land in LDS once the stages are reused
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+
+  // epilogue: lane holds rows 16 ms + 4 kq + e of its fragments' column lr
+  const int4 d = c.d;
+  if (kMode == kModeGateUp) {
+    // h, and -136 * sum(h) per 128 columns: waves 0-3 cover the tile's first 128 columns,
+    // waves 4-7 the second; per-wave row partials meet in LDS (activation stage 0)
+    float* red = reinterpret_cast<float*>(lds.a[0]);  // [kWaves][kTileM]
+    __syncthreads();  // every wave is done reading the activation stages
+#pragma unroll
+    for (int ms = 0; ms < NSUB; ++ms) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = ms * 16 + 4 * kq + e;
+        const bool valid = r < c.rows;
+        const int m = d.w + min(r, c.rows - 1);
+        const int hrow = c.shared ? p.T * p.top_k + m : d.y + m;
+        float part = 0.f;
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+          const int col = c.nt * 256 + wave * 32 + f * 16 + lr;
+          const uint16_t hb = f32_to_bf16(silu(u[ms][f][e] * s_prev[f]) * (u[ms][f + 2][e] * s_prev[f + 2]));
+          if (valid) p.out_bf16[static_cast<int64_t>(hrow) * inter + octet_slot(col)] = hb;
+          part += bf16_to_f32(hb);
+        }
+        part = row16_sum(part);
+        if (lr == 0) red[wave * kTileM + r] = part;
+      }
+    }
+    __syncthreads();
+    if (tid < 2 * kTileM) {
+      const int half = tid >= kTileM ? 1 : 0, r = tid - half * kTileM;
+      if (r < c.rows) {
+        const float* q = red + 4 * half * kTileM + r;
+        const float sum = (q[0] + q[kTileM]) + (q[2 * kTileM] + q[3 * kTileM]);
+        const int m = d.w + r;
+        const int hrow = c.shared ? p.T * p.top_k + m : d.y + m;
+        p.out_part[static_cast<int64_t>(hrow) * (inter >> 7) + c.nt * 2 + half] = -kDequantOffset * sum;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int ms = 0; ms < NSUB; ++ms) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = ms * 16 + 4 * kq + e;
+        if (r >= c.rows) continue;
+        const int m = d.w + r;
+        const int yrow = c.shared ? p.T * p.top_k + m : d.y + m;
+        const float wgt = c.shared ? p.shared_gate[m] : p.slot_w[d.y + m];
+        float* o = p.out_f32 + static_cast<int64_t>(yrow) * p.N + c.nt * kTileN + wave * 64 + lr;
+#pragma unroll
+        for (int f = 0; f < 4; ++f) o[f * 16] = u[ms][f][e] * s_prev[f] * wgt;
+      }
+    }
+  }
+}
+
+}  // namespace
+
+template <int kMode, typename ScaleT>
+__global__ __launch_bounds__(512) void w4_tile_kernel(W4StreamParams p) {
+  __shared__ uint4 a0[kBlocks * 64], a1[kBlocks * 64];
+  __shared__ float n0[128], n1[128];
+  __shared__ uint4 w0[kWaves * 4 * 64], w1[kWaves * 4 * 64], w2[kWaves * 4 * 64];
+  __shared__ uint32_t s0[kWaves * 64], s1[kWaves * 64], s2[kWaves * 64];
+  const TileLds lds{{a0, a1}, {n0, n1}, {w0, w1, w2}, {s0, s1, s2}};
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = lane_id(), lr = lane & 15, kq = lane >> 4;
+  const int K = p.K, nkb = K >> 7, ng = K / p.G;
+  const uint32_t rb = static_cast<uint32_t>(K >> 1);
+  const int total_passes = ld_const(p.meta, 1);
+  const int ntiles = p.strips;  // column tiles per pass
+  const int total = total_passes * ntiles;
+  const int inter = p.N >> 1;
+  // activation rows: tokens (gate_up) or every routed slot row plus the shared expert's (down)
+  const uint32_t act_rows = kMode == kModeGateUp ? p.T : p.T * p.top_k + (p.has_shared ? p.T : 0);
+  const buf_rsrc ars = make_rsrc(p.act, act_rows * static_cast<uint32_t>(K) * 2);
+  const buf_rsrc nrs = make_rsrc(p.act_neg, act_rows * static_cast<uint32_t>(nkb) * 4);
+
+  // weight row of fragment f, column lc (0..15) of this wave in column tile nt
+  auto wrow = [&](int nt, int f, int lc) {
+    return kMode == kModeGateUp ? (f >> 1) * inter + nt * 256 + wave * 32 + (f & 1) * 16 + lc
+                                : nt * kTileN + wave * 64 + f * 16 + lc;
+  };
+
+  for (int tile = blockIdx.x; tile < total; tile += gridDim.x) {
+    TileCtx c;
+    const int P = tile / ntiles;
+    c.nt = tile - P * ntiles;
+    c.d = ld_const_int4(p.pass_table, P);
+    c.shared = c.d.x < 0;
+    c.rows = min(kTileM, c.d.z - c.d.w);
+    c.ars = ars;
+    c.nrs = nrs;
+    c.wrs = make_rsrc(c.shared ? p.w_shared : p.w + static_cast<int64_t>(c.d.x) * p.w_stride,
+                      static_cast<uint32_t>(p.N) * rb);
+    c.srs = make_rsrc(static_cast<const uint8_t*>(c.shared ? p.s_shared : p.s) +
+                          (c.shared ? 0 : static_cast<int64_t>(c.d.x) * p.s_stride * static_cast<int64_t>(sizeof(ScaleT))),
+                      static_cast<uint32_t>(p.N) * static_cast<uint32_t>(ng) * sizeof(ScaleT));
+#pragma unroll
+    for (int f = 0; f < 4; ++f) c.woff[f] = static_cast<uint32_t>(wrow(c.nt, f, lr)) * rb + kq * 16;
+    c.soff = static_cast<uint32_t>(wrow(c.nt, lane >> 4, lr)) * static_cast<uint32_t>(ng) * sizeof(ScaleT);
+
+    // source row of pass row r (rows past the pass repeat its last row)
+    auto src_row = [&](int r) {
+      const int m = c.d.w + min(r, c.rows - 1);
+      if (kMode == kModeGateUp) return c.shared ? m : p.tok[c.d.y + m];
+      return c.shared ? p.T * p.top_k + m : c.d.y + m;
+    };
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      const int b = wave + kWaves * i;  // block: subtile b / 4, k-step b % 4
+      c.aoff[i] = static_cast<uint32_t>(src_row(16 * (b >> 2) + lr)) * static_cast<uint32_t>(K) * 2 +
+                  (4 * kq + (b & 3)) * 16;
+    }
+    c.noff = static_cast<uint32_t>(src_row(min(wave * 64 + lane, kTileM - 1))) * static_cast<uint32_t>(nkb) * 4;
+
+    __syncthreads();  // the previous tile's readers are done with every LDS stage
+
+    switch ((c.rows + 15) >> 4) {
+      case 1: tile_pass<kMode, ScaleT, 1>(p, lds, c); break;
+      case 2: tile_pass<kMode, ScaleT, 2>(p, lds, c); break;
+      case 3: tile_pass<kMode, ScaleT, 3>(p, lds, c); break;
+      case 4: tile_pass<kMode, ScaleT, 4>(p, lds, c); break;
+      case 5: tile_pass<kMode, ScaleT, 5>(p, lds, c); break;
+      default: tile_pass<kMode, ScaleT, 6>(p, lds, c); break;
+    }
+  }
+}
+
+bool w4_tile_supports(int mode, int N, int K, int G) {
+  if (K % 512 || (G != 128 && G != 256)) return false;
+  return mode == kModeGateUp ? (N / 2) % 256 == 0 : (mode == kModeDown && N % kTileN == 0);
+}
+
+void launch_w4_tile(int mode, bool fp32_scales, int grid, const W4StreamParams& p, hipStream_t stream) {
+  const dim3 g(static_cast<unsigned>(grid)), blk(512);
+  if (mode == kModeGateUp) {
+    if (fp32_scales) hipLaunchKernelGGL((w4_tile_kernel<kModeGateUp, float>), g, blk, 0, stream, p);
+    else hipLaunchKernelGGL((w4_tile_kernel<kModeGateUp, uint16_t>), g, blk, 0, stream, p);
+  } else {
+    if (fp32_scales) hipLaunchKernelGGL((w4_tile_kernel<kModeDown, float>), g, blk, 0, stream, p);
+    else hipLaunchKernelGGL((w4_tile_kernel<kModeDown, uint16_t>), g, blk, 0, stream, p);
+  }
+}
+
+}  // namespace dflash

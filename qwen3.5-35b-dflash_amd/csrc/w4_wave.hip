@@ -34,12 +34,14 @@ constexpr int kWaveLdsA = 139264;     // activation rows (row stride 2K + 16 byt
 constexpr int kWaveLdsNeg = 2048;     // -136*sum terms, floats
 constexpr int kWaveLdsTok = 2048;     // token of every routed slot row (kModeGateUp)
 constexpr int kWaveLdsWgt = 512;      // routing weights of the chunk rows (kModeDown)
+constexpr int kWaveLdsPass = 64;      // pass descriptors of the workgroup's range (or down chunk)
 
 struct WaveLds {
   uint4 a[kWaveLdsA / 16];
   float neg[kWaveLdsNeg];
   int tok[kWaveLdsTok];
   float wgt[kWaveLdsWgt];
+  int4 pdesc[kWaveLdsPass];
 };
 
 template <int kNKB, typename ScaleT>
@@ -80,12 +82,15 @@ __device__ __forceinline__ float row_scale(const uint32_t* words, int kb) {
 // Opaque to the optimiser: the value must exist in registers at this point.
 __device__ __forceinline__ void pin(f32x4& v) { asm volatile("" : "+v"(v)); }
 
-// k-block prefetch distance and units per unrolled loop iteration.
+// k-block prefetch distance and units per unrolled loop iteration.  Loads run
+// kDepth - 1 k-blocks ahead and may cross into later units; the scale ring
+// holds one slot per unit of the iteration, enough for the computed unit and
+// every unit with loads in flight, and every ring index is compile-time.
 template <int kNKB>
 struct WavePipe {
-  static constexpr int kDepth = 4;  // loads run at most one unit ahead
-  static constexpr int kUnits = 2;                  // scale ring of two units
-  static_assert(kDepth <= kNKB, "the prefetch must stay within the next unit");
+  static constexpr int kDepth = kNKB >= 8 ? 4 : 6;
+  static constexpr int kUnits = kNKB >= 8 ? 2 : 3;
+  static_assert(1 + (kDepth - 1 + kNKB - 1) / kNKB <= kUnits, "scale ring too small for the prefetch distance");
   static_assert((kUnits * kNKB) % kDepth == 0, "buffer indices must be compile-time");
 };
 
@@ -116,8 +121,18 @@ __global__ __launch_bounds__(512) void w4_wave_kernel(W4StreamParams p) {
   const uint32_t wlane = static_cast<uint32_t>(lr * rb + kq * 16);     // lane offset inside a tile
   const uint32_t slane = static_cast<uint32_t>(lr * kNKB * sizeof(ScaleT));
 
-  auto pass_desc = [&](int P) -> int4 {
+  // Pass descriptors come from LDS once staged (a scalar load would make the
+  // next LDS wait, which shares its counter, wait for it too); only the first
+  // unit of a chunk, issued before the staging barrier, reads them with s_load.
+  int pd_base = 0, pd_count = 0;
+  auto pass_desc = [&](int P, bool staged) -> int4 {
     if (kMode == kModeLinear) return make_int4(0, 0, p.M, P * 16);
+    const int i = P - pd_base;
+    if (staged && i >= 0 && i < pd_count) {
+      const int4 v = lds.pdesc[i];
+      return make_int4(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
+                       __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w));
+    }
     return ld_const_int4(p.pass_table, P);
   };
 
@@ -141,12 +156,13 @@ __global__ __launch_bounds__(512) void w4_wave_kernel(W4StreamParams p) {
     int4 l_d = make_int4(0, 0, 0, 0);
     const uint8_t* l_w = nullptr;
     const uint8_t* l_s = nullptr;
+    bool staged = false;  // pass descriptors of this chunk are in LDS
     auto load_unit_bases = [&]() {
       const int u = cb + wave + 8 * l_t;
       const int P = u / strips, strip = u - P * strips;
       if (P != l_P) {
         l_P = P;
-        l_d = pass_desc(P);
+        l_d = pass_desc(P, staged);
       }
       const bool shared = kMode != kModeLinear && l_d.x < 0;
       const int64_t e = kMode == kModeLinear ? 0 : l_d.x;
@@ -178,8 +194,13 @@ __global__ __launch_bounds__(512) void w4_wave_kernel(W4StreamParams p) {
     if (n_mine > 0) {
       load_unit_bases();
 #pragma unroll
-      for (int i = 0; i + 1 < kDepth; ++i) issue(wbuf[i], sbuf[0], i);
+      for (int i = 0; i + 1 < kDepth; ++i) issue(wbuf[i], sbuf[(i / kNKB) % kUnits], i % kNKB);
     }
+
+    // descriptors of the passes this chunk covers
+    pd_base = Pc;
+    pd_count = min(Pc_end - Pc, kWaveLdsPass);
+    if (kMode != kModeLinear && tid < pd_count) lds.pdesc[tid] = p.pass_table[Pc + tid];
 
     if (kMode != kModeDown && Pc == P_first) {
       // x rows (octet-interleaved), their -136*sum terms, the token of every
@@ -264,6 +285,7 @@ __global__ __launch_bounds__(512) void w4_wave_kernel(W4StreamParams p) {
       }
     }
     __syncthreads();
+    staged = true;
     if (n_mine == 0) continue;
 
     // compute state
@@ -291,7 +313,7 @@ __global__ __launch_bounds__(512) void w4_wave_kernel(W4StreamParams p) {
             strip = u - P * strips;
             if (P != c_P) {
               c_P = P;
-              c_d = pass_desc(P);
+              c_d = pass_desc(P, true);
             }
             const int M = c_d.z, m0 = c_d.w;
             const int ma = min(m0 + lr, M - 1);

@@ -92,6 +92,8 @@ def test_moe_prefill_t2048(pkg, device):
     (20, 16, 4, 1024, 1024, 128, torch.float32, True),        # small-T kernel: K = 1024 both ways, fp32 scales
     (32, 64, 8, 2048, 512, 128, torch.bfloat16, True),        # small-T kernel at its largest T
     (9, 8, 8, 512, 512, 128, torch.bfloat16, True),           # small-T kernel, E == k
+    (300, 16, 4, 1024, 512, 128, torch.float32, True),        # tiled prefill kernel, fp32 scales
+    (256, 8, 2, 2048, 512, 256, torch.bfloat16, False),       # tiled prefill kernel, group 256
 ])
 def test_moe_small_shapes(pkg, device, tokens, experts, k, hidden, inter, group, scale_dtype, shared):
     print(f"moe T={tokens} E={experts} k={k} H={hidden} I={inter} g={group} {scale_dtype} shared={shared}",
