@@ -76,8 +76,8 @@ RouteLayout route_layout(int64_t T, int64_t k, int64_t E) {
   L.tok = c.take(4 * static_cast<size_t>(T * k + 1));
   // counts and the slot map are contiguous: one clearing pass covers both
   L.counts = c.off;
-  L.slotmap = L.counts + 4 * static_cast<size_t>(E);
-  c.take(4 * static_cast<size_t>(E) + static_cast<size_t>(E) * T + 4);
+  L.slotmap = L.counts + 4 * static_cast<size_t>((E + 3) & ~3);
+  c.take(4 * static_cast<size_t>(dflash::route_zero_words(static_cast<int>(T), static_cast<int>(E))) + 16);
   L.total = c.off;
   return L;
 }
@@ -415,7 +415,8 @@ int dflash_router_logits(const void* hidden, int64_t tokens, int64_t hidden_size
     f.T = static_cast<int>(tokens);
     f.E = static_cast<int>(experts);
     f.H = static_cast<int>(hidden_size);
-    f.n_router = static_cast<int>(((tokens + 15) / 16) * ((experts + 15) / 16));
+    f.router_big = dflash::router_big_fits(f.T, f.H) ? 1 : 0;
+    f.n_router = dflash::router_tiles(f.T, f.E, f.H);
     dflash::launch_front(f, static_cast<hipStream_t>(stream));
     return launch_status("router");
   } catch (...) {
@@ -536,7 +537,8 @@ int dflash_moe_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, co
     f.T = T;
     f.E = E;
     f.H = static_cast<int>(S.H);
-    f.n_router = router_logits ? 0 : ((T + 15) / 16) * ((E + 15) / 16);
+    f.router_big = dflash::router_big_fits(T, f.H) ? 1 : 0;
+    f.n_router = router_logits ? 0 : dflash::router_tiles(T, E, f.H);
     f.prep_rows = T;
     f.x_il = at<uint16_t>(workspace, L.x_il);
     f.xneg = at<float>(workspace, L.xneg);

@@ -23,6 +23,7 @@ struct FrontParams {
   float* logits;            // fp32 [T][E]
   int T, E, H;
   int n_router;             // router tiles (0 when the logits are given)
+  int router_big;           // 32 x 64 tiles (router_big_fits) instead of 16 x 16
   int prep_rows;            // rows of x to prepare (T, or 0 for router tiles only)
   uint16_t* x_il;           // octet-interleaved copy of x [T][H]
   float* xneg;              // -136 * sum per 128-column block [T][H/128]
@@ -45,7 +46,7 @@ struct RouteParams {
   int32_t* pass_start;  // [E+2] first pass of each slot, then the total
   int32_t* meta;        // [0] hit experts, [1] total passes
   int32_t* counts;      // [E], followed in memory by the slot map (multi-workgroup path)
-  uint8_t* slotmap;     // [E][T]
+  uint8_t* slotmap;     // [E][route_slot_pitch(T)] bytes: slot + 1 of token t in expert e, or 0; 16-byte aligned
   int4* slot_table;     // [E+1] per slot: expert (-1 shared), segment start, rows, first pass
   int32_t* pass_slot;   // [T*k + T] slot of every pass
   int4* pass_table;     // [T*k + T] per pass: expert (-1 shared), segment start, slot rows, first row of the pass
@@ -125,7 +126,12 @@ struct W4StreamParams {
 };
 
 void launch_front(const FrontParams& p, hipStream_t stream);
+// Router tiles of a launch: 32 tokens x 64 experts when T >= 64 and H % 128 == 0, else 16 x 16.
+bool router_big_fits(int T, int H);
+int router_tiles(int T, int E, int H);
 bool route_small_fits(int T, int E, int k);
+// Row pitch of the multi-workgroup slot map: T rounded up to 16 bytes.
+__host__ __device__ inline int route_slot_pitch(int T) { return (T + 15) & ~15; }
 int64_t route_zero_words(int T, int E);
 void launch_route(const RouteParams& p, bool zeroed, hipStream_t stream);
 void launch_table_prep(const TableParams& p, hipStream_t stream);

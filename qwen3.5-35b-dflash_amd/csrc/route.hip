@@ -15,10 +15,17 @@
 // expert as one more slot) and, per slot, the first "pass" index, a pass being
 // up to rows_per_pass of the slot's tokens.
 #include <algorithm>
+#include <utility>
 
 #include "kernels.h"
 
 namespace dflash {
+
+// f(integral_constant<int, I>) for every I of the sequence, in order.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for(std::integer_sequence<int, I...>, F&& f) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
 
 // ---------------------------------------------------------------------------
 // DPP helpers (64-bit max over a wave without LDS round trips).
@@ -156,6 +163,64 @@ __device__ __forceinline__ void prep_row(const uint16_t* __restrict__ x, int K, 
   }
 }
 
+// Rows per prep block: 2 for short inputs (more blocks in flight), 16 for long ones.
+__host__ __device__ inline int prep_rows_per_block(int rows) { return rows <= 64 ? 2 : 16; }
+
+// Activation preparation of up to 16 rows by a 512-thread block: thread half h
+// handles rows r0 + 2i + h, and the loads of all its rows are issued before any
+// of them is written back, so a block waits for memory once per 2048 columns.
+__device__ __forceinline__ void prep_block(const uint16_t* __restrict__ x, int K, int r0, int nrows,
+                                           uint16_t* __restrict__ x_il, float* __restrict__ xneg,
+                                           const uint16_t* __restrict__ gate_w, float* __restrict__ gate_out) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  __shared__ float part[16][4];
+  const int tid = threadIdx.x, h = tid >> 8, t = tid & 255, wave = tid >> 6;
+  const int chunks = K >> 3;
+  const u32x4 zero4 = {0u, 0u, 0u, 0u};
+  float gacc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) gacc[i] = 0.f;
+  for (int base = 0; base < chunks; base += 256) {
+    const int c = base + t;
+    const u32x4 g = gate_w && c < chunks ? reinterpret_cast<const u32x4*>(gate_w)[c] : zero4;
+    u32x4 v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = r0 + min(2 * i + h, nrows - 1);
+      v[i] = c < chunks ? reinterpret_cast<const u32x4*>(x + static_cast<int64_t>(r) * K)[c] : zero4;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = r0 + 2 * i + h;
+      const bool live = 2 * i + h < nrows && c < chunks;
+      u32x4 o;  // natural pairs (0,1)(2,3)(4,5)(6,7) -> (0,4)(1,5)(2,6)(3,7)
+      o.x = (v[i].x & 0xFFFFu) | (v[i].z << 16);
+      o.y = (v[i].x >> 16) | (v[i].z & 0xFFFF0000u);
+      o.z = (v[i].y & 0xFFFFu) | (v[i].w << 16);
+      o.w = (v[i].y >> 16) | (v[i].w & 0xFFFF0000u);
+      if (live) reinterpret_cast<u32x4*>(x_il + static_cast<int64_t>(r) * K)[c] = o;
+      float sum = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float lo = __uint_as_float(v[i][q] << 16), hi = __uint_as_float(v[i][q] & 0xFFFF0000u);
+        sum += lo + hi;
+        gacc[i] += lo * __uint_as_float(g[q] << 16) + hi * __uint_as_float(g[q] & 0xFFFF0000u);
+      }
+      sum = row16_sum(sum);  // 16 chunks of 8 = one 128-column block, in 16 consecutive lanes
+      if (live && (c & 15) == 0) xneg[static_cast<int64_t>(r) * (K >> 7) + (c >> 4)] = -kDequantOffset * sum;
+    }
+  }
+  if (gate_w) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float s = wave_sum(gacc[i]);
+      if (lane_id() == 0) part[2 * i + h][wave & 3] = s;
+    }
+    __syncthreads();
+    if (tid < nrows) gate_out[r0 + tid] = 1.0f / (1.0f + __expf(-((part[tid][0] + part[tid][1]) + (part[tid][2] + part[tid][3]))));
+  }
+}
+
 // Router logits for a 16x16 tile: fp32 [T][E] = x bf16 [T][H] . W bf16 [E][H]^T;
 // 8 waves split H (H % 256 == 0) and are reduced through LDS.
 __device__ __forceinline__ void router_tile(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
@@ -196,23 +261,99 @@ __device__ __forceinline__ void router_tile(const uint16_t* __restrict__ x, cons
   }
 }
 
+// Router logits for a 32-token x 64-expert tile (long T): the 128-column chunks
+// of both operands are staged once in LDS in MFMA fragment order (8 KB + 16 KB
+// per stage, two stages), fed from registers that keep kAhead chunks in
+// flight, and each of the 8 waves computes one 16 x 16 block over the whole of
+// H (H % 128 == 0).
+__device__ __forceinline__ void router_big_tile(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                float* __restrict__ logits, int T, int E, int H, int t0, int e0) {
+  constexpr int kAhead = 8;
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // a plain vector: the ring stays in registers
+  __shared__ u32x4 sa[2][2 * 4 * 64];  // [stage][token subtile x k-step][lane]
+  __shared__ u32x4 sb[2][4 * 4 * 64];  // [stage][expert subtile x k-step][lane]
+  const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id();
+  const int lr = lane & 15, kq = lane >> 4, tq = wave & 1, eq = wave >> 1;
+  // staging: thread copies 16-byte chunk sc of token row sr and of expert rows sr and 32 + sr
+  const int sr = tid >> 4, sc = tid & 15;
+  const u32x4* ga = reinterpret_cast<const u32x4*>(x + static_cast<int64_t>(min(t0 + sr, T - 1)) * H) + sc;
+  const u32x4* gb0 = reinterpret_cast<const u32x4*>(w + static_cast<int64_t>(min(e0 + sr, E - 1)) * H) + sc;
+  const u32x4* gb1 = reinterpret_cast<const u32x4*>(w + static_cast<int64_t>(min(e0 + 32 + sr, E - 1)) * H) + sc;
+  // fragment slot of (row r, chunk c): block (r / 16) * 4 + c / 4, lane r % 16 + 16 * (c % 4)
+  const int frag = (sc >> 2) * 64 + (sr & 15) + 16 * (sc & 3);
+  const int slot0 = (sr >> 4) * 4 * 64 + frag, slot1 = ((sr + 32) >> 4) * 4 * 64 + frag;
+  const int nch = H >> 7;
+  // the ring is indexed through static_for so its slots are constants before unrolling (registers)
+  u32x4 ra[kAhead], rb0[kAhead], rb1[kAhead];
+  static_for(std::make_integer_sequence<int, kAhead>{}, [&](auto ic) __attribute__((always_inline)) {
+    constexpr int i = decltype(ic)::value;
+    const int c = min(i, nch - 1) * 16;  // past the end: a repeat, never stored
+    ra[i] = ga[c];
+    rb0[i] = gb0[c];
+    rb1[i] = gb1[c];
+  });
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int ch0 = 0; ch0 < nch; ch0 += kAhead) {
+    static_for(std::make_integer_sequence<int, kAhead>{}, [&](auto ic) __attribute__((always_inline)) {
+      constexpr int i = decltype(ic)::value;
+      const int ch = ch0 + i;
+      if (ch < nch) {
+        constexpr int st = i & 1;  // stage st was last read two chunks ago, before the previous barrier
+        sa[st][slot0] = ra[i];
+        sb[st][slot0] = rb0[i];
+        sb[st][slot1] = rb1[i];
+        __syncthreads();
+        const int c = min(ch + kAhead, nch - 1) * 16;
+        ra[i] = ga[c];
+        rb0[i] = gb0[c];
+        rb1[i] = gb1[c];
+        u32x4 fa[4], fb[4];  // all fragments of the chunk first: one LDS wait, then the MFMA chain
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          fa[j] = sa[st][(tq * 4 + j) * 64 + lane];
+          fb[j] = sb[st][(eq * 4 + j) * 64 + lane];
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // 8 LDS reads, then 4 MFMAs
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc = mfma16x16x32(__builtin_bit_cast(uint4, fa[j]), __builtin_bit_cast(uint4, fb[j]), acc);
+      }
+    });
+  }
+  const int e = e0 + eq * 16 + lr;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = t0 + tq * 16 + 4 * kq + i;
+    if (t < T && e < E) logits[static_cast<int64_t>(t) * E + e] = acc[i];
+  }
+}
+
 // One launch doing the work that needs no routing: router tiles (optional),
 // activation prep rows, and zeroing of the multi-workgroup routing buffers.
-// block = 512.  blocks: [0, n_router) router tiles, then prep_rows prep rows,
+// block = 512.  blocks: [0, n_router) router tiles, then prep blocks (prep_rows_per_block rows),
 // then n_zero blocks clearing zero_words 32-bit words.
 __global__ __launch_bounds__(512) void front_kernel(FrontParams p) {
   int b = blockIdx.x;
   if (b < p.n_router) {
-    const int tiles_e = (p.E + 15) / 16;
-    router_tile(p.x, p.router_w, p.logits, p.T, p.E, p.H, (b / tiles_e) * 16, (b % tiles_e) * 16);
+    if (p.router_big) {
+      const int tiles_e = (p.E + 63) / 64;
+      router_big_tile(p.x, p.router_w, p.logits, p.T, p.E, p.H, (b / tiles_e) * 32, (b % tiles_e) * 64);
+    } else {
+      const int tiles_e = (p.E + 15) / 16;
+      router_tile(p.x, p.router_w, p.logits, p.T, p.E, p.H, (b / tiles_e) * 16, (b % tiles_e) * 16);
+    }
     return;
   }
   b -= p.n_router;
-  if (b < p.prep_rows) {
-    prep_row(p.x, p.H, b, p.x_il, p.xneg, p.gate_w, p.gate_out);
+  const int per_block = prep_rows_per_block(p.prep_rows);
+  const int prep_blocks = (p.prep_rows + per_block - 1) / per_block;
+  if (b < prep_blocks) {
+    prep_block(p.x, p.H, per_block * b, min(per_block, p.prep_rows - per_block * b), p.x_il, p.xneg, p.gate_w,
+               p.gate_out);
     return;
   }
-  b -= p.prep_rows;
+  b -= prep_blocks;
   for (int64_t i = static_cast<int64_t>(b) * 512 + threadIdx.x; i < p.zero_words;
        i += static_cast<int64_t>(p.n_zero) * 512)
     p.zero[i] = 0u;
@@ -332,16 +473,59 @@ __global__ __launch_bounds__(256) void route_topk_kernel(RouteParams p) {
   if (lane < p.k) {
     p.ids[static_cast<int64_t>(t) * p.k + lane] = id;
     p.wts[static_cast<int64_t>(t) * p.k + lane] = w;
-    atomicAdd(&p.counts[id], 1);
-    p.slotmap[static_cast<int64_t>(id) * p.T + t] = static_cast<uint8_t>(lane + 1);
+    p.slotmap[static_cast<int64_t>(id) * route_slot_pitch(p.T) + t] = static_cast<uint8_t>(lane + 1);
   }
 }
 
-// grid = ceil(E/4), block = 256: one wave per expert.
+// Non-zero bytes of a 32-bit word.
+__device__ __forceinline__ int nonzero_bytes(uint32_t x) {
+  const uint32_t zero_hi = ~(((x & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | x | 0x7F7F7F7Fu);  // 0x80 per zero byte
+  return 4 - __popc(zero_hi);
+}
+
+__device__ __forceinline__ int nonzero_bytes(uint4 v) {
+  return nonzero_bytes(v.x) + nonzero_bytes(v.y) + nonzero_bytes(v.z) + nonzero_bytes(v.w);
+}
+
+// grid = ceil(E/4), block = 256: one wave per expert counts its tokens in the slot map.
+__global__ __launch_bounds__(256) void route_count_kernel(RouteParams p) {
+  const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (e >= p.E) return;
+  const int chunks = route_slot_pitch(p.T) >> 4;
+  const uint4* row = reinterpret_cast<const uint4*>(p.slotmap + static_cast<int64_t>(e) * route_slot_pitch(p.T));
+  int n = 0;
+  for (int c = lane_id(); c < chunks; c += 64) n += nonzero_bytes(row[c]);
+  n = wave_sum_int(n);
+  if (lane_id() == 0) p.counts[e] = n;
+}
+
+// Exclusive prefix sum over the wave's lanes.
+__device__ __forceinline__ int wave_exclusive_scan(int v) {
+  const int lane = lane_id();
+  int incl = v;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += u;
+  }
+  return incl - v;
+}
+
+// grid = ceil(E/4), block = 256: one wave per expert writes its segment of the
+// permutation.  Lane l owns a contiguous run of the expert's slot-map row, so
+// an exclusive scan of the per-lane hit counts gives every token its position
+// in ascending token order.
 __global__ __launch_bounds__(256) void route_permute_kernel(RouteParams p) {
   const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = lane_id();
   if (e >= p.E) return;
+  // this lane's run of the slot-map row (kept in registers for runs of up to 2 chunks), loaded
+  // before the count prefix so both latencies overlap
+  const int pitch = route_slot_pitch(p.T);
+  const int per_lane = ((pitch >> 4) + 63) >> 6;  // 16-byte chunks per lane
+  const uint4* row = reinterpret_cast<const uint4*>(p.slotmap + static_cast<int64_t>(e) * pitch);
+  const int c0 = lane * per_lane, c1 = min(c0 + per_lane, pitch >> 4);
+  const uint4 zero4 = make_uint4(0u, 0u, 0u, 0u);
+  const uint4 r0 = c0 < c1 ? row[c0] : zero4, r1 = c0 + 1 < c1 ? row[c0 + 1] : zero4;
   int before = 0, nz_before = 0, pass_before = 0;
   for (int i = lane; i < e; i += 64) {
     const int c = p.counts[i];
@@ -375,24 +559,28 @@ __global__ __launch_bounds__(256) void route_permute_kernel(RouteParams p) {
     }
   }
   if (cnt == 0) return;
-  const uint8_t* row = p.slotmap + static_cast<int64_t>(e) * p.T;
-  int running = 0;
-  for (int t0 = 0; t0 < p.T; t0 += 64) {
-    const int t = t0 + lane;
-    const int slot1 = t < p.T ? row[t] : 0;
-    const uint64_t mask = __ballot(slot1 != 0);
-    if (slot1) {
-      const int pos = before + running + __popcll(mask & ((1ull << lane) - 1ull));
-      const int flat = t * p.k + slot1 - 1;
-      p.perm[pos] = flat;
-      p.inv[flat] = pos;
-      p.slot_w[pos] = p.wts[flat];
-      p.tok[pos] = t;
+  int mine = nonzero_bytes(r0) + nonzero_bytes(r1);
+  for (int c = c0 + 2; c < c1; ++c) mine += nonzero_bytes(row[c]);
+  int pos = before + wave_exclusive_scan(mine);
+  for (int c = c0; c < c1 && mine > 0; ++c) {
+    const uint4 v = c == c0 ? r0 : c == c0 + 1 ? r1 : row[c];
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int slot1 = (w[q >> 2] >> (8 * (q & 3))) & 0xFF;
+      if (slot1) {
+        const int t = 16 * c + q;
+        const int flat = t * p.k + slot1 - 1;
+        p.perm[pos] = flat;
+        p.inv[flat] = pos;
+        p.slot_w[pos] = p.wts[flat];
+        p.tok[pos] = t;
+        ++pos;
+        --mine;
+      }
     }
-    running += __popcll(mask);
   }
 }
-
 // ---------------------------------------------------------------------------
 // Work table from existing segment offsets (experts-only entry) plus the
 // activation prep rows.  block = 512: block 0 builds the table (E <= 1024
@@ -501,8 +689,15 @@ __global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ y
 
 // ---------------------------------------------------------------------------
 // host launchers
+bool router_big_fits(int T, int H) { return T >= 64 && H % 128 == 0; }
+
+int router_tiles(int T, int E, int H) {
+  return router_big_fits(T, H) ? ((T + 31) / 32) * ((E + 63) / 64) : ((T + 15) / 16) * ((E + 15) / 16);
+}
+
 void launch_front(const FrontParams& p, hipStream_t stream) {
-  const int blocks = p.n_router + p.prep_rows + p.n_zero;
+  const int per_block = prep_rows_per_block(p.prep_rows);
+  const int blocks = p.n_router + (p.prep_rows + per_block - 1) / per_block + p.n_zero;
   if (blocks <= 0) return;
   hipLaunchKernelGGL(front_kernel, dim3(blocks), dim3(512), 0, stream, p);
 }
@@ -512,8 +707,8 @@ bool route_small_fits(int T, int E, int k) {
 }
 
 int64_t route_zero_words(int T, int E) {
-  // counts [E] followed by the slot map [E][T] bytes, in 32-bit words
-  return E + (static_cast<int64_t>(E) * T + 3) / 4;
+  // counts [E rounded up to 4] followed by the slot map [E][pitch] bytes, in 32-bit words
+  return ((E + 3) & ~3) + static_cast<int64_t>(E) * route_slot_pitch(T) / 4;
 }
 
 void launch_route(const RouteParams& p, bool zeroed, hipStream_t stream) {
@@ -528,6 +723,7 @@ void launch_route(const RouteParams& p, bool zeroed, hipStream_t stream) {
                        reinterpret_cast<uint32_t*>(p.counts), words);
   }
   if (p.T > 0) hipLaunchKernelGGL(route_topk_kernel, dim3((p.T + 3) / 4), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL(route_count_kernel, dim3((p.E + 3) / 4), dim3(256), 0, stream, p);
   hipLaunchKernelGGL(route_permute_kernel, dim3((p.E + 3) / 4), dim3(256), 0, stream, p);
 }
 

@@ -86,3 +86,16 @@ def test_router_logits(pkg, device, tokens):
     golden = oracle_moe.router_logits(layer.hidden, layer.router_weight)
     report = metrics.compare(got, golden)
     assert report["max_rel"] <= 1e-5, report
+
+
+@pytest.mark.parametrize("tokens,experts,hidden", [(100, 100, 1024), (65, 200, 768)])
+def test_router_logits_ragged_tiles(pkg, device, tokens, experts, hidden):
+    """Token and expert counts that leave partial 32 x 64 router tiles."""
+    print(f"router T={tokens} E={experts} H={hidden}", flush=True)
+    gen = torch.Generator().manual_seed(tokens + experts)
+    x = torch.randn((tokens, hidden), generator=gen).to(torch.bfloat16)
+    w = (0.02 * torch.randn((experts, hidden), generator=gen)).to(torch.bfloat16)
+    got = pkg.ops.router_logits(x.to(device), w.to(device)).cpu()
+    golden = oracle_moe.router_logits(x, w)
+    report = metrics.compare(got, golden)
+    assert report["max_rel"] <= 1e-5, report
