@@ -27,32 +27,6 @@ __device__ __forceinline__ void static_for(std::integer_sequence<int, I...>, F&&
   (f(std::integral_constant<int, I>{}), ...);
 }
 
-// ---------------------------------------------------------------------------
-// DPP helpers (64-bit max over a wave without LDS round trips).
-template <int kCtrl>
-__device__ __forceinline__ uint64_t dpp64(uint64_t v) {
-  const uint32_t lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(v), kCtrl, 0xF, 0xF, false);
-  const uint32_t hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(v >> 32), kCtrl, 0xF, 0xF, false);
-  return (static_cast<uint64_t>(hi) << 32) | lo;
-}
-
-__device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
-
-__device__ __forceinline__ uint64_t readlane64(uint64_t v, int lane) {
-  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(v), lane);
-  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(v >> 32), lane);
-  return (static_cast<uint64_t>(hi) << 32) | lo;
-}
-
-// Max over all 64 lanes, returned wave-uniform.
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-  v = umax64(v, dpp64<0xB1>(v));   // quad_perm [1,0,3,2]
-  v = umax64(v, dpp64<0x4E>(v));   // quad_perm [2,3,0,1]
-  v = umax64(v, dpp64<0x141>(v));  // row_half_mirror
-  v = umax64(v, dpp64<0x140>(v));  // row_mirror: every lane of a 16-lane row holds the row max
-  return umax64(umax64(readlane64(v, 0), readlane64(v, 16)), umax64(readlane64(v, 32), readlane64(v, 48)));
-}
-
 // Order-preserving uint32 of a float: -0 folded to +0, NaN ranks below -inf.
 __device__ __forceinline__ uint32_t sortable_key(float f) {
   uint32_t u = __float_as_uint(f);
@@ -65,33 +39,53 @@ __device__ __forceinline__ float key_to_float(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 
-// Top-k of one token's logits by one wave: k rounds of a wave-wide 64-bit max
-// over (key << 32 | ~id), so the larger logit wins and, among equal logits,
-// the lower expert id.  Lane s < k ends with (id_s, weight_s).
+// Max of a 32-bit value over all 64 lanes, returned wave-uniform.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  auto dmax = [](uint32_t x, uint32_t y) { return x > y ? x : y; };
+  v = dmax(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xB1, 0xF, 0xF, false)));
+  v = dmax(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x4E, 0xF, 0xF, false)));
+  v = dmax(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x141, 0xF, 0xF, false)));
+  v = dmax(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x140, 0xF, 0xF, false)));
+  const uint32_t a = __builtin_amdgcn_readlane(static_cast<int>(v), 0), b = __builtin_amdgcn_readlane(static_cast<int>(v), 16);
+  const uint32_t c = __builtin_amdgcn_readlane(static_cast<int>(v), 32), d = __builtin_amdgcn_readlane(static_cast<int>(v), 48);
+  return dmax(dmax(a, b), dmax(c, d));
+}
+
+// Top-k of one token's logits by one wave.  Lane l holds experts l + 64 i as
+// 32-bit keys (sortable_key + 1; 0 marks padding and experts already taken).
+// Each of the k rounds takes the wave-wide maximum key, then the lowest
+// expert id holding it (a ballot per block of 64 ids, first set bit of the
+// first non-empty block): the larger logit wins and, among equal logits, the
+// lower expert id.  Lane s < k ends with (id_s, weight_s).
 template <int kPer>
 __device__ __forceinline__ void wave_topk(const float* __restrict__ row, int E, int k, int* id_out, float* w_out) {
   const int lane = lane_id();
-  uint64_t key[kPer];
+  uint32_t key[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int e = lane + 64 * i;
-    key[i] = (e < E) ? ((static_cast<uint64_t>(sortable_key(row[e])) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(e)))
-                     : 0ull;
+    key[i] = e < E ? sortable_key(row[e]) + 1u : 0u;  // sortable keys stay below 0xFF800001
   }
   int my_id = -1;
   uint32_t my_key = 0;
   for (int s = 0; s < k; ++s) {
-    uint64_t best = key[0];
+    uint32_t m = key[0];
 #pragma unroll
-    for (int i = 1; i < kPer; ++i) best = umax64(best, key[i]);
-    best = wave_max_u64(best);
-    const int e = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(best));
+    for (int i = 1; i < kPer; ++i) m = m > key[i] ? m : key[i];
+    m = wave_max_u32(m);
+    int e = -1;
+#pragma unroll
+    for (int i = kPer - 1; i >= 0; --i) {  // the lowest block with a hit decides
+      const uint64_t hits = __ballot(key[i] == m);
+      if (hits) e = 64 * i + __builtin_ctzll(hits);
+    }
+    e = __builtin_amdgcn_readfirstlane(e);
 #pragma unroll
     for (int i = 0; i < kPer; ++i)
-      if (lane + 64 * i == e) key[i] = 0ull;
+      if (lane + 64 * i == e) key[i] = 0u;
     if (lane == s) {
       my_id = e;
-      my_key = static_cast<uint32_t>(best >> 32);
+      my_key = m - 1u;
     }
   }
   const float top = key_to_float(__builtin_amdgcn_readlane(static_cast<int>(my_key), 0));

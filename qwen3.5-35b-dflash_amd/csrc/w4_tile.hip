@@ -280,78 +280,81 @@ __device__ __forceinline__ void tile_pass(const W4StreamParams& p, const TileLds
   }
 }
 
-}  // namespace
-
+// One work tile: pass P (up to 96 rows of one slot) times column tile nt.
 template <int kMode, typename ScaleT>
-__global__ __launch_bounds__(512) void w4_tile_kernel(W4StreamParams p) {
-  __shared__ uint4 a0[kBlocks * 64], a1[kBlocks * 64];
-  __shared__ float n0[128], n1[128];
-  __shared__ uint4 w0[kWaves * 4 * 64], w1[kWaves * 4 * 64], w2[kWaves * 4 * 64];
-  __shared__ uint32_t s0[kWaves * 64], s1[kWaves * 64], s2[kWaves * 64];
-  const TileLds lds{{a0, a1}, {n0, n1}, {w0, w1, w2}, {s0, s1, s2}};
-
+__device__ __forceinline__ void run_tile(const W4StreamParams& p, const TileLds& lds, int P, int nt) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = lane_id(), lr = lane & 15, kq = lane >> 4;
   const int K = p.K, nkb = K >> 7, ng = K / p.G;
   const uint32_t rb = static_cast<uint32_t>(K >> 1);
-  const int total_passes = ld_const(p.meta, 1);
-  const int ntiles = p.strips;  // column tiles per pass
-  const int total = total_passes * ntiles;
   const int inter = p.N >> 1;
   // activation rows: tokens (gate_up) or every routed slot row plus the shared expert's (down)
   const uint32_t act_rows = kMode == kModeGateUp ? p.T : p.T * p.top_k + (p.has_shared ? p.T : 0);
-  const buf_rsrc ars = make_rsrc(p.act, act_rows * static_cast<uint32_t>(K) * 2);
-  const buf_rsrc nrs = make_rsrc(p.act_neg, act_rows * static_cast<uint32_t>(nkb) * 4);
 
-  // weight row of fragment f, column lc (0..15) of this wave in column tile nt
-  auto wrow = [&](int nt, int f, int lc) {
+  // weight row of fragment f, column lc (0..15) of this wave
+  auto wrow = [&](int f, int lc) {
     return kMode == kModeGateUp ? (f >> 1) * inter + nt * 256 + wave * 32 + (f & 1) * 16 + lc
                                 : nt * kTileN + wave * 64 + f * 16 + lc;
   };
 
+  TileCtx c;
+  c.nt = nt;
+  c.d = ld_const_int4(p.pass_table, P);
+  c.shared = c.d.x < 0;
+  c.rows = min(kTileM, c.d.z - c.d.w);
+  c.ars = make_rsrc(p.act, act_rows * static_cast<uint32_t>(K) * 2);
+  c.nrs = make_rsrc(p.act_neg, act_rows * static_cast<uint32_t>(nkb) * 4);
+  c.wrs = make_rsrc(c.shared ? p.w_shared : p.w + static_cast<int64_t>(c.d.x) * p.w_stride,
+                    static_cast<uint32_t>(p.N) * rb);
+  c.srs = make_rsrc(static_cast<const uint8_t*>(c.shared ? p.s_shared : p.s) +
+                        (c.shared ? 0 : static_cast<int64_t>(c.d.x) * p.s_stride * static_cast<int64_t>(sizeof(ScaleT))),
+                    static_cast<uint32_t>(p.N) * static_cast<uint32_t>(ng) * sizeof(ScaleT));
+#pragma unroll
+  for (int f = 0; f < 4; ++f) c.woff[f] = static_cast<uint32_t>(wrow(f, lr)) * rb + kq * 16;
+  c.soff = static_cast<uint32_t>(wrow(lane >> 4, lr)) * static_cast<uint32_t>(ng) * sizeof(ScaleT);
+
+  // source row of pass row r (rows past the pass repeat its last row)
+  auto src_row = [&](int r) {
+    const int m = c.d.w + min(r, c.rows - 1);
+    if (kMode == kModeGateUp) return c.shared ? m : p.tok[c.d.y + m];
+    return c.shared ? p.T * p.top_k + m : c.d.y + m;
+  };
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const int b = wave + kWaves * i;  // block: subtile b / 4, k-step b % 4
+    c.aoff[i] = static_cast<uint32_t>(src_row(16 * (b >> 2) + lr)) * static_cast<uint32_t>(K) * 2 +
+                (4 * kq + (b & 3)) * 16;
+  }
+  c.noff = static_cast<uint32_t>(src_row(min(wave * 64 + lane, kTileM - 1))) * static_cast<uint32_t>(nkb) * 4;
+
+  __syncthreads();  // the previous tile's readers are done with every LDS stage
+
+  switch ((c.rows + 15) >> 4) {
+    case 1: tile_pass<kMode, ScaleT, 1>(p, lds, c); break;
+    case 2: tile_pass<kMode, ScaleT, 2>(p, lds, c); break;
+    case 3: tile_pass<kMode, ScaleT, 3>(p, lds, c); break;
+    case 4: tile_pass<kMode, ScaleT, 4>(p, lds, c); break;
+    case 5: tile_pass<kMode, ScaleT, 5>(p, lds, c); break;
+    default: tile_pass<kMode, ScaleT, 6>(p, lds, c); break;
+  }
+}
+
+}  // namespace
+
+template <int kMode, typename ScaleT>
+__global__ __launch_bounds__(512) void w4_tile_kernel(W4StreamParams p) {
+  // the stages, a separate LDS array each
+  __shared__ uint4 a0[kBlocks * 64], a1[kBlocks * 64];
+  __shared__ float n0[128], n1[128];
+  __shared__ uint4 w0[kWaves * 4 * 64], w1[kWaves * 4 * 64], w2[kWaves * 4 * 64];
+  __shared__ uint32_t s0[kWaves * 64], s1[kWaves * 64], s2[kWaves * 64];
+  const TileLds lds{{a0, a1}, {n0, n1}, {w0, w1, w2}, {s0, s1, s2}};
+  const int ntiles = p.strips;  // column tiles per pass
+  const int total = ld_const(p.meta, 1) * ntiles;
   for (int tile = blockIdx.x; tile < total; tile += gridDim.x) {
-    TileCtx c;
     const int P = tile / ntiles;
-    c.nt = tile - P * ntiles;
-    c.d = ld_const_int4(p.pass_table, P);
-    c.shared = c.d.x < 0;
-    c.rows = min(kTileM, c.d.z - c.d.w);
-    c.ars = ars;
-    c.nrs = nrs;
-    c.wrs = make_rsrc(c.shared ? p.w_shared : p.w + static_cast<int64_t>(c.d.x) * p.w_stride,
-                      static_cast<uint32_t>(p.N) * rb);
-    c.srs = make_rsrc(static_cast<const uint8_t*>(c.shared ? p.s_shared : p.s) +
-                          (c.shared ? 0 : static_cast<int64_t>(c.d.x) * p.s_stride * static_cast<int64_t>(sizeof(ScaleT))),
-                      static_cast<uint32_t>(p.N) * static_cast<uint32_t>(ng) * sizeof(ScaleT));
-#pragma unroll
-    for (int f = 0; f < 4; ++f) c.woff[f] = static_cast<uint32_t>(wrow(c.nt, f, lr)) * rb + kq * 16;
-    c.soff = static_cast<uint32_t>(wrow(c.nt, lane >> 4, lr)) * static_cast<uint32_t>(ng) * sizeof(ScaleT);
-
-    // source row of pass row r (rows past the pass repeat its last row)
-    auto src_row = [&](int r) {
-      const int m = c.d.w + min(r, c.rows - 1);
-      if (kMode == kModeGateUp) return c.shared ? m : p.tok[c.d.y + m];
-      return c.shared ? p.T * p.top_k + m : c.d.y + m;
-    };
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      const int b = wave + kWaves * i;  // block: subtile b / 4, k-step b % 4
-      c.aoff[i] = static_cast<uint32_t>(src_row(16 * (b >> 2) + lr)) * static_cast<uint32_t>(K) * 2 +
-                  (4 * kq + (b & 3)) * 16;
-    }
-    c.noff = static_cast<uint32_t>(src_row(min(wave * 64 + lane, kTileM - 1))) * static_cast<uint32_t>(nkb) * 4;
-
-    __syncthreads();  // the previous tile's readers are done with every LDS stage
-
-    switch ((c.rows + 15) >> 4) {
-      case 1: tile_pass<kMode, ScaleT, 1>(p, lds, c); break;
-      case 2: tile_pass<kMode, ScaleT, 2>(p, lds, c); break;
-      case 3: tile_pass<kMode, ScaleT, 3>(p, lds, c); break;
-      case 4: tile_pass<kMode, ScaleT, 4>(p, lds, c); break;
-      case 5: tile_pass<kMode, ScaleT, 5>(p, lds, c); break;
-      default: tile_pass<kMode, ScaleT, 6>(p, lds, c); break;
-    }
+    run_tile<kMode, ScaleT>(p, lds, P, tile - P * ntiles);
   }
 }
 
