@@ -67,7 +67,8 @@ def device_bank(pkg, gen, shape, device):
     return pkg.PackedW4(packed, scales.to(torch.bfloat16).contiguous(), 128)
 
 
-def weight_sets(pkg, nsets, device, seed=1234, hidden=2048, inter=512, experts=256):
+def weight_sets(pkg, nsets, device, seed=1234, hidden=2048, inter=512, experts=256, tiled=True):
+    """Random banks per set; repacked once into the kernels' tiled layout (as a model load would) unless tiled=False."""
     gen = torch.Generator(device=device).manual_seed(seed)
     sets = []
     for _ in range(nsets):
@@ -77,7 +78,10 @@ def weight_sets(pkg, nsets, device, seed=1234, hidden=2048, inter=512, experts=2
                               device_bank(pkg, gen, (hidden, inter), device),
                               (torch.randn((hidden,), device=device, generator=gen) * 0.02).to(torch.bfloat16))
         router = (torch.randn((experts, hidden), device=device, generator=gen) * 0.02).to(torch.bfloat16)
+        if tiled:
+            gu, dn, sh = gu.tiled(), dn.tiled(), sh.tiled()
         sets.append((gu, dn, sh, router))
+    torch.cuda.synchronize()
     return sets
 
 
@@ -282,7 +286,8 @@ def main() -> int:
         "layer_hbm_frac_int4": round(layer_gbs / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "w4_wave_kernel<1, 16, unsigned short> (grouped gate/up + SiLU*up, T=16)",
+                     "kernel": "w4_verify_kernel<1, 16, unsigned short> (grouped gate/up + SiLU*up, T=16, "
+                               "tiled banks)",
                      "kernel_us": round(gu_ms * 1e3, 2), "hit_experts_mean": round(gu_hits, 2),
                      "bytes_per_launch": int(gu_bytes)},
         "stages": {"expert_stage_us": round(exp_ms * 1e3, 2), "down_kernel_us": round(dn_ms * 1e3, 2),

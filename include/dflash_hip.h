@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define DFLASH_ABI_VERSION 1
+#define DFLASH_ABI_VERSION 2
 
 enum dflash_status {
   DFLASH_OK = 0,
@@ -40,16 +40,41 @@ enum dflash_status {
 
 enum dflash_dtype { DFLASH_DTYPE_BF16 = 0, DFLASH_DTYPE_F32 = 1 };
 
+/*
+ * Byte order of a packed bank (same sizes either way):
+ *   PORTABLE  the reference format above: packed [experts][rows][cols/2], scales
+ *             [experts][rows][cols/group_size].
+ *   TILED     this library's streaming order, made once by dflash_w4_to_tiled():
+ *             per expert, per tile of 16 rows t and per 128-column block b, one
+ *             contiguous 1 KB block whose byte 16*l + j (l = 0..63) is portable
+ *             byte 64*b + 16*(l / 16) + j of row 16*t + l % 16; scales per expert
+ *             [rows/16][cols/group_size][16], element [t][g][c] = portable [16*t + c][g].
+ *             Every 64-lane 16-byte load of the expert kernels is then one
+ *             contiguous kilobyte.  Needs rows % 16 == 0 and cols % 128 == 0.
+ */
+enum dflash_layout { DFLASH_LAYOUT_PORTABLE = 0, DFLASH_LAYOUT_TILED = 1 };
+
 /* One packed int4 matrix (experts == 1) or expert bank (experts == E). */
 typedef struct dflash_w4 {
-  const void* packed;  /* uint8 [experts][rows][cols/2] */
-  const void* scales;  /* [experts][rows][cols/group_size], scale_dtype */
+  const void* packed;  /* uint8, experts * rows * cols / 2 bytes in `layout` order */
+  const void* scales;  /* experts * rows * cols / group_size elements of scale_dtype, in `layout` order */
   int64_t experts;
   int64_t rows;        /* N: output features */
   int64_t cols;        /* K: input features */
   int64_t group_size;  /* 128 or 256 */
   int32_t scale_dtype; /* enum dflash_dtype */
+  int32_t layout;      /* enum dflash_layout */
 } dflash_w4;
+
+/*
+ * Repack a PORTABLE matrix or bank into the TILED layout (same shape fields,
+ * group size and scale dtype; packed_out and scales_out are the caller's, the
+ * size of src's arrays).  A one-time step at weight-load time, like the vendor
+ * path's conversion to its own int4 layout (fused/quantization.py:112-115
+ * expects I4ZN [K, N/8] for npu_quant_matmul); it has no counterpart in the
+ * CPU reference.  Constraints: rows % 16 == 0, cols % 128 == 0.
+ */
+int dflash_w4_to_tiled(const dflash_w4* src, void* packed_out, void* scales_out, void* stream);
 
 /* ABI version of the loaded library (DFLASH_ABI_VERSION). */
 int dflash_abi_version(void);

@@ -9,7 +9,14 @@ nibbles ``q[2j]`` in bits 0-3 and ``q[2j+1]`` in bits 4-7.  Scales are
 ``[..., N, K/G]``, one per group of ``G`` consecutive K values; the dequantised
 weight is ``q[n, k] * s[n, k // G]``.
 
-Pinning: ``pack``/``unpack`` by brute force over all 16 nibble values in both
+The *tiled* layout (this build's own streaming order, defined in
+``include/dflash_hip.h``; no counterpart in the reference) is restated by
+``to_tiled``: per ``[..., 16-row tile t, 128-column block b]`` one kilobyte whose
+16-byte chunk ``l`` is bytes ``64 b + 16 (l // 16) ..+15`` of row ``16 t + l % 16``;
+scales ``[..., N/16, K/G, 16]``.
+
+Pinning: ``to_tiled`` by a per-byte brute force of that definition on small
+banks and by ``from_tiled`` (its inverse) round trips; ``pack``/``unpack`` by brute force over all 16 nibble values in both
 positions and by the hand-written known-answer bytes in
 ``tests/golden/w4_golden.json``; ``quantize`` by the known-answer groups in the
 same file (written by an independent pure-Python restatement); ``qlinear`` by
@@ -102,3 +109,34 @@ def qlinear(x: torch.Tensor, packed, scales, group_size: int, *, accumulate: str
     if accumulate == "fp32":
         return (torch.from_numpy(xv) @ torch.from_numpy(w).T).numpy()
     raise ValueError("accumulate must be fp64 or fp32")
+
+
+def to_tiled(packed: np.ndarray, scales: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Portable ``packed [..., N, K/2]``, ``scales [..., N, K/G]`` -> the tiled order, same shapes."""
+    packed = np.asarray(packed)
+    scales = np.asarray(scales)
+    *lead, n, half = packed.shape
+    k = half * 2
+    if n % 16 or k % 128:
+        raise ValueError("the tiled layout needs N % 16 == 0 and K % 128 == 0")
+    groups = scales.shape[-1]
+    # [..., t, r, b, q, 16 bytes] -> [..., t, b, q, r, 16 bytes]: chunk l = 16 q + r
+    chunks = packed.reshape(*lead, n // 16, 16, k // 128, 4, 16)
+    tiled = np.moveaxis(chunks, -4, -2).reshape(packed.shape)
+    s = scales.reshape(*lead, n // 16, 16, groups)
+    tiled_s = np.swapaxes(s, -1, -2).reshape(scales.shape)
+    return np.ascontiguousarray(tiled), np.ascontiguousarray(tiled_s)
+
+
+def from_tiled(packed: np.ndarray, scales: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Inverse of ``to_tiled``."""
+    packed = np.asarray(packed)
+    scales = np.asarray(scales)
+    *lead, n, half = packed.shape
+    k = half * 2
+    groups = scales.shape[-1]
+    chunks = packed.reshape(*lead, n // 16, k // 128, 4, 16, 16)
+    portable = np.moveaxis(chunks, -2, -4).reshape(packed.shape)
+    s = scales.reshape(*lead, n // 16, groups, 16)
+    portable_s = np.swapaxes(s, -1, -2).reshape(scales.shape)
+    return np.ascontiguousarray(portable), np.ascontiguousarray(portable_s)

@@ -12,9 +12,11 @@ from pathlib import Path
 PACKAGE_DIR = Path(__file__).resolve().parent
 LIBRARY_PATH = PACKAGE_DIR / "libdflash_hip.so"
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 DTYPE_BF16 = 0
 DTYPE_F32 = 1
+LAYOUT_PORTABLE = 0
+LAYOUT_TILED = 1
 
 STATUS_NAMES = {
     1: "DFLASH_ERR_INVALID_ARGUMENT",
@@ -40,6 +42,7 @@ class W4Desc(ctypes.Structure):
         ("cols", ctypes.c_int64),
         ("group_size", ctypes.c_int64),
         ("scale_dtype", ctypes.c_int32),
+        ("layout", ctypes.c_int32),
     ]
 
 
@@ -47,6 +50,7 @@ _W4P = ctypes.POINTER(W4Desc)
 
 SIGNATURES = {
     "dflash_abi_version": (ctypes.c_int, []),
+    "dflash_w4_to_tiled": (ctypes.c_int, [_W4P, _P, _P, _P]),
     "dflash_last_error": (ctypes.c_char_p, []),
     "dflash_qlinear_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
     "dflash_qlinear_w4a16": (ctypes.c_int, [_P, _I64, _W4P, _P, _P, _SZ, _P]),

@@ -55,7 +55,19 @@ int check_w4(const dflash_w4* w, const char* name, int64_t experts, int64_t rows
   if (w->group_size != 128 && w->group_size != 256)
     return fail(DFLASH_ERR_UNSUPPORTED, std::string(name) + ": group_size must be 128 or 256");
   if (cols % w->group_size) return fail(DFLASH_ERR_INVALID_ARGUMENT, std::string(name) + ": K not a multiple of group_size");
+  if (w->layout != DFLASH_LAYOUT_PORTABLE && w->layout != DFLASH_LAYOUT_TILED)
+    return fail(DFLASH_ERR_INVALID_ARGUMENT, std::string(name) + ": layout must be PORTABLE or TILED");
+  if (w->layout == DFLASH_LAYOUT_TILED && (rows % 16 || cols % 128))
+    return fail(DFLASH_ERR_INVALID_ARGUMENT, std::string(name) + ": the tiled layout needs rows % 16 == 0 and cols % 128 == 0");
   return DFLASH_OK;
+}
+
+// The wave-streaming and per-wave fallback kernels read portable rows only.
+int tiled_unsupported(const char* what) {
+  return fail(DFLASH_ERR_UNSUPPORTED, std::string(what) +
+                                          ": tiled weights are streamed by the verify, streaming and tile kernels "
+                                          "only (group size 128 for T <= 32 and the streaming path); use the "
+                                          "portable layout for this shape");
 }
 
 // ---------------------------------------------------------------- layouts
@@ -141,6 +153,7 @@ struct MoeShapes {
   bool shared;
   bool gu_f32, dn_f32;
   bool scales16;  // every scale bank 16-byte aligned (row scales load as 16-byte words)
+  bool tiled;     // every bank in the tiled layout
 };
 
 bool moe_wave_path(const MoeShapes& S) {
@@ -184,16 +197,21 @@ int check_moe(const void* hidden, int64_t T, int64_t H, int64_t k, const dflash_
     if (int r = check_w4(sgu, "shared_gate_up", 1, 2 * I, H)) return r;
     if (int r = check_w4(sdn, "shared_down", 1, H, I)) return r;
     if (sgu->group_size != gate_up->group_size || sdn->group_size != down->group_size ||
-        sgu->scale_dtype != gate_up->scale_dtype || sdn->scale_dtype != down->scale_dtype)
-      return fail(DFLASH_ERR_UNSUPPORTED, "shared expert must use the routed banks' group sizes and scale dtypes");
+        sgu->scale_dtype != gate_up->scale_dtype || sdn->scale_dtype != down->scale_dtype ||
+        sgu->layout != gate_up->layout || sdn->layout != gate_up->layout)
+      return fail(DFLASH_ERR_UNSUPPORTED,
+                  "shared expert must use the routed banks' group sizes, scale dtypes and layout");
     if (!aligned16(sgate)) return fail(DFLASH_ERR_INVALID_ARGUMENT, "shared_gate_weight not 16-byte aligned");
   }
   if (T > 0 && (!hidden || !out)) return fail(DFLASH_ERR_INVALID_ARGUMENT, "hidden and out are required");
   if (!aligned16(hidden) || !aligned16(out)) return fail(DFLASH_ERR_INVALID_ARGUMENT, "hidden/out not 16-byte aligned");
   const bool scales16 = aligned16(gate_up->scales) && aligned16(down->scales) &&
                         (!shared || (aligned16(sgu->scales) && aligned16(sdn->scales)));
+  if (gate_up->layout != down->layout)
+    return fail(DFLASH_ERR_UNSUPPORTED, "gate_up and down must share one layout");
   *S = MoeShapes{T, H, I, E, k, gate_up->group_size, down->group_size, shared,
-                 gate_up->scale_dtype == DFLASH_DTYPE_F32, down->scale_dtype == DFLASH_DTYPE_F32, scales16};
+                 gate_up->scale_dtype == DFLASH_DTYPE_F32, down->scale_dtype == DFLASH_DTYPE_F32, scales16,
+                 gate_up->layout == DFLASH_LAYOUT_TILED};
   return DFLASH_OK;
 }
 
@@ -235,15 +253,144 @@ void launch_w4(int mode, bool fp32_scales, int mt, int max_slots, GemmPath path,
   }
 }
 
+// Whether launch_w4 would run a kernel that reads the tiled layout (tile, or the
+// streaming kernel when it splits this K); the wave and per-wave fallbacks do not.
+bool w4_path_reads_tiled(int mode, int N, int K, int G, GemmPath path) {
+  using namespace dflash;
+  if (path == GemmPath::kTile) return true;
+  if (path == GemmPath::kWave) return false;
+  const int cols = mode == kModeGateUp ? N / 2 / 16 : N / 32;
+  return w4_stream_supports(K, G) && cols % w4_stream_row_groups(K) == 0;
+}
+
+// Verify-block path (T <= 32): both expert GEMMs on w4_verify, the gate/up
+// launch routing in its prologue when `route` is asked for and fits, the down
+// launch running the combine.  False when the shapes need the other kernels.
+bool verify_fits(const MoeShapes& S, bool route, dflash::VerifyParams* gu, dflash::VerifyParams* dn) {
+  using namespace dflash;
+  if (!moe_wave_path(S)) return false;
+  const int T = static_cast<int>(S.T), H = static_cast<int>(S.H), I = static_cast<int>(S.I);
+  const int E = static_cast<int>(S.E), k = static_cast<int>(S.k), sh = S.shared ? 1 : 0;
+  *gu = VerifyParams{};
+  *dn = VerifyParams{};
+  return verify_layout(kModeGateUp, T, H, 2 * I, E, k, sh, route ? 1 : 0, gu) &&
+         verify_layout(kModeDown, T, I, H, E, k, sh, 0, dn);
+}
+
+// Routing outputs the gate/up launch writes when it routes in its prologue.
+struct RouteOut {
+  const float* logits;
+  int32_t* ids;
+  float* wts;
+  int32_t* perm;
+  int32_t* inv;
+  int32_t* offsets;
+};
+
+int run_verify(const MoeShapes& S, dflash::VerifyParams gu, dflash::VerifyParams dn, const RouteOut& ro,
+               const int32_t* inv, void* ws, const MoeLayout& L, const dflash_w4* gate_up, const dflash_w4* down,
+               const dflash_w4* sgu, const dflash_w4* sdn, void* out, hipStream_t stream) {
+  using namespace dflash;
+  const int T = static_cast<int>(S.T), H = static_cast<int>(S.H), I = static_cast<int>(S.I);
+  W4StreamParams p{};
+  p.pass_table = at<int4>(ws, L.route.pass_table);
+  p.tok = at<int32_t>(ws, L.route.tok);
+  p.meta = at<int32_t>(ws, L.route.meta);
+  p.top_k = static_cast<int>(S.k);
+  p.T = T;
+  p.has_shared = S.shared ? 1 : 0;
+  p.rows_per_pass = 16;
+  p.tiled = S.tiled ? 1 : 0;
+
+  // gate_up: N = 2I rows over K = H, SiLU*up epilogue into h
+  p.w = static_cast<const uint8_t*>(gate_up->packed);
+  p.s = gate_up->scales;
+  p.w_shared = S.shared ? static_cast<const uint8_t*>(sgu->packed) : nullptr;
+  p.s_shared = S.shared ? sgu->scales : nullptr;
+  p.w_stride = S.I * S.H;
+  p.s_stride = 2 * S.I * (S.H / 128);
+  p.N = 2 * I;
+  p.K = H;
+  p.G = 128;
+  p.act = at<uint16_t>(ws, L.x_il);
+  p.act_neg = at<float>(ws, L.xneg);
+  p.neg_parts = 1;
+  p.out_bf16 = at<uint16_t>(ws, L.h);
+  p.out_part = at<float>(ws, L.hpart);
+  p.strips = I / 16;
+  gu.g = p;
+  gu.E = static_cast<int>(S.E);
+  // measurement mode times the GEMM on the work table an earlier full call left
+  if (measuring()) gu.route = 0;
+  if (gu.route) {
+    gu.logits = ro.logits;
+    gu.ids = ro.ids;
+    gu.wts = ro.wts;
+    gu.perm = ro.perm;
+    gu.inv = ro.inv;
+    gu.offsets = ro.offsets;
+    gu.meta_out = at<int32_t>(ws, L.route.meta);
+    gu.pass_table_out = at<int4>(ws, L.route.pass_table);
+    gu.slot_w_out = at<float>(ws, L.route.slot_w);
+    gu.tok_out = at<int32_t>(ws, L.route.tok);
+  }
+  if (stage_on(DFLASH_STAGE_GATE_UP)) launch_w4_verify(kModeGateUp, S.gu_f32, cu_count(), gu, stream);
+  if (int r = launch_status("gate_up")) return r;
+
+  // down: N = H rows over K = I, routing-weight epilogue into y, then the combine
+  p.w = static_cast<const uint8_t*>(down->packed);
+  p.s = down->scales;
+  p.w_shared = S.shared ? static_cast<const uint8_t*>(sdn->packed) : nullptr;
+  p.s_shared = S.shared ? sdn->scales : nullptr;
+  p.w_stride = S.H * S.I / 2;
+  p.s_stride = S.H * (S.I / 128);
+  p.N = H;
+  p.K = I;
+  p.act = at<uint16_t>(ws, L.h);
+  p.act_neg = at<float>(ws, L.hpart);
+  p.neg_parts = 8;
+  p.out_bf16 = nullptr;
+  p.out_part = nullptr;
+  p.out_f32 = at<float>(ws, L.y);
+  p.slot_w = at<float>(ws, L.route.slot_w);
+  p.shared_gate = at<float>(ws, L.gate);
+  p.strips = H / 32;
+  dn.g = p;
+  dn.E = static_cast<int>(S.E);
+  if (stage_on(DFLASH_STAGE_DOWN)) launch_w4_verify(kModeDown, S.dn_f32, cu_count(), dn, stream);
+  if (int r = launch_status("down")) return r;
+
+  if (measuring()) return DFLASH_OK;
+  launch_combine(at<float>(ws, L.y), inv, T, p.top_k, H, p.has_shared, static_cast<uint16_t*>(out), stream);
+  return launch_status("combine");
+}
+
 // gate_up -> down -> combine for a routing and work table already in place.
 // Every kernel input besides x and the weight banks comes from the workspace
 // (routing kernels or table_prep wrote it); inv (the caller's) feeds combine.
+GemmPath moe_gemm_path(const MoeShapes& S) {
+  return moe_wave_path(S) ? GemmPath::kWave : moe_tile_path(S) ? GemmPath::kTile : GemmPath::kStream;
+}
+
+// Tiled banks need every expert kernel of the call to read that layout; checked
+// before anything is launched.
+int check_tiled_moe(const MoeShapes& S, bool verify) {
+  using namespace dflash;
+  if (!S.tiled || verify) return DFLASH_OK;
+  const GemmPath path = moe_gemm_path(S);
+  const int H = static_cast<int>(S.H), I = static_cast<int>(S.I);
+  if (!w4_path_reads_tiled(kModeGateUp, 2 * I, H, static_cast<int>(S.G), path) ||
+      !w4_path_reads_tiled(kModeDown, H, I, static_cast<int>(S.Gd), path))
+    return tiled_unsupported("moe");
+  return DFLASH_OK;
+}
+
 int run_experts(const MoeShapes& S, const int32_t* inv, void* ws, const MoeLayout& L, const dflash_w4* gate_up,
                 const dflash_w4* down, const dflash_w4* sgu, const dflash_w4* sdn, void* out, hipStream_t stream) {
   using namespace dflash;
   const int T = static_cast<int>(S.T), H = static_cast<int>(S.H), I = static_cast<int>(S.I);
   const int k = static_cast<int>(S.k);
-  const GemmPath path = moe_wave_path(S) ? GemmPath::kWave : moe_tile_path(S) ? GemmPath::kTile : GemmPath::kStream;
+  const GemmPath path = moe_gemm_path(S);
   const int mt = path == GemmPath::kStream ? token_tiles(S.T) : 1;
   const int32_t* meta = at<int32_t>(ws, L.route.meta);
   const int4* slot_table = at<int4>(ws, L.route.slot_table);
@@ -258,6 +405,7 @@ int run_experts(const MoeShapes& S, const int32_t* inv, void* ws, const MoeLayou
   p.T = T;
   p.has_shared = S.shared ? 1 : 0;
   p.rows_per_pass = rows_per_pass(S);
+  p.tiled = S.tiled ? 1 : 0;
   const int max_slots = static_cast<int>(std::min<int64_t>(S.E, S.T * S.k)) + p.has_shared;
 
   // gate_up: N = 2I rows over K = H, SiLU*up epilogue into h
@@ -338,6 +486,34 @@ extern "C" {
 
 int dflash_abi_version(void) { return DFLASH_ABI_VERSION; }
 
+int dflash_w4_to_tiled(const dflash_w4* src, void* packed_out, void* scales_out, void* stream) {
+  try {
+    if (!src) return fail(DFLASH_ERR_INVALID_ARGUMENT, "to_tiled: descriptor is NULL");
+    if (src->experts <= 0 || src->rows <= 0 || src->cols <= 0)
+      return fail(DFLASH_ERR_INVALID_ARGUMENT, "to_tiled: experts, rows and cols must be positive");
+    if (int r = check_w4(src, "to_tiled", src->experts, src->rows, src->cols)) return r;
+    if (src->layout != DFLASH_LAYOUT_PORTABLE) return fail(DFLASH_ERR_INVALID_ARGUMENT, "to_tiled: source must be PORTABLE");
+    if (src->rows % 16 || src->cols % 128)
+      return fail(DFLASH_ERR_UNSUPPORTED, "to_tiled: needs rows % 16 == 0 and cols % 128 == 0");
+    if (src->rows > (1 << 30) || src->cols > (1 << 30))
+      return fail(DFLASH_ERR_UNSUPPORTED, "to_tiled: rows and cols must stay below 2^30");
+    if (!packed_out || !scales_out || !aligned16(packed_out))
+      return fail(DFLASH_ERR_INVALID_ARGUMENT, "to_tiled: outputs NULL or packed_out not 16-byte aligned");
+    const size_t sal = src->scale_dtype == DFLASH_DTYPE_F32 ? 4u : 2u;
+    if (reinterpret_cast<uintptr_t>(scales_out) % sal)
+      return fail(DFLASH_ERR_INVALID_ARGUMENT, "to_tiled: scales_out misaligned");
+    if (packed_out == src->packed || scales_out == src->scales)
+      return fail(DFLASH_ERR_INVALID_ARGUMENT, "to_tiled: outputs must not alias the source");
+    dflash::launch_tile_w4(src->packed, src->scales, src->scale_dtype == DFLASH_DTYPE_F32, src->experts,
+                           static_cast<int>(src->rows), static_cast<int>(src->cols),
+                           static_cast<int>(src->group_size), packed_out, scales_out,
+                           static_cast<hipStream_t>(stream));
+    return launch_status("to_tiled");
+  } catch (...) {
+    return fail(DFLASH_ERR_HIP, "unexpected host exception");
+  }
+}
+
 const char* dflash_last_error(void) { return g_last_error.c_str(); }
 
 size_t dflash_qlinear_workspace_bytes(int64_t m, int64_t k, int64_t group_size) {
@@ -364,6 +540,20 @@ int dflash_qlinear_w4a16(const void* x, int64_t m, const dflash_w4* weight, void
     if (!workspace || workspace_bytes < need || !aligned16(workspace))
       return fail(DFLASH_ERR_WORKSPACE, "qlinear workspace needs " + std::to_string(need) + " bytes");
     hipStream_t st = static_cast<hipStream_t>(stream);
+    // GEMM kernel: verify (m <= 32, group 128), else wave-streaming for portable weights
+    // that fit, else the streaming kernel (or its per-wave fallback)
+    const bool tiled = weight->layout == DFLASH_LAYOUT_TILED;
+    dflash::VerifyParams vl{};
+    const bool verify = weight->group_size == 128 && aligned16(weight->scales) &&
+                        dflash::verify_layout(dflash::kModeLinear, static_cast<int>(m), static_cast<int>(K),
+                                              static_cast<int>(N), 1, 1, 0, 0, &vl);
+    const bool wave = !verify && !tiled && aligned16(weight->scales) &&
+                      dflash::w4_wave_supports(dflash::kModeLinear, static_cast<int>(K),
+                                               static_cast<int>(weight->group_size), static_cast<int>(m));
+    if (tiled && !verify &&
+        !w4_path_reads_tiled(dflash::kModeLinear, static_cast<int>(N), static_cast<int>(K),
+                             static_cast<int>(weight->group_size), GemmPath::kStream))
+      return tiled_unsupported("qlinear");
     Carver c;
     uint16_t* x_il = at<uint16_t>(workspace, c.take(2 * static_cast<size_t>(m) * K));
     float* xneg = at<float>(workspace, c.take(4 * static_cast<size_t>(m) * (K / 128)));
@@ -379,6 +569,7 @@ int dflash_qlinear_w4a16(const void* x, int64_t m, const dflash_w4* weight, void
     dflash::W4StreamParams p{};
     p.w = static_cast<const uint8_t*>(weight->packed);
     p.s = weight->scales;
+    p.tiled = weight->layout == DFLASH_LAYOUT_TILED ? 1 : 0;
     p.N = static_cast<int>(N);
     p.K = static_cast<int>(K);
     p.G = static_cast<int>(weight->group_size);
@@ -387,8 +578,13 @@ int dflash_qlinear_w4a16(const void* x, int64_t m, const dflash_w4* weight, void
     p.neg_parts = 1;
     p.out_bf16 = static_cast<uint16_t*>(y);
     p.M = static_cast<int>(m);
-    const bool wave = aligned16(weight->scales) &&
-                      dflash::w4_wave_supports(dflash::kModeLinear, p.K, p.G, static_cast<int>(m));
+    if (verify) {
+      p.rows_per_pass = 16;
+      p.strips = p.N / 32;
+      vl.g = p;
+      dflash::launch_w4_verify(dflash::kModeLinear, weight->scale_dtype == DFLASH_DTYPE_F32, cu_count(), vl, st);
+      return launch_status("qlinear");
+    }
     const int mt = wave ? 1 : token_tiles(m);
     p.rows_per_pass = 16 * mt;
     launch_w4(dflash::kModeLinear, weight->scale_dtype == DFLASH_DTYPE_F32, mt, 1, wave ? GemmPath::kWave : GemmPath::kStream,
@@ -496,8 +692,14 @@ int dflash_moe_experts_w4a16(const void* hidden, int64_t tokens, int64_t hidden_
     t.xneg = at<float>(workspace, L.xneg);
     t.gate_w = S.shared ? static_cast<const uint16_t*>(shared_gate_weight) : nullptr;
     t.gate_out = at<float>(workspace, L.gate);
+    dflash::VerifyParams vgu, vdn;
+    const bool verify = verify_fits(S, false, &vgu, &vdn);
+    if (int r = check_tiled_moe(S, verify)) return r;
     if (!measuring()) dflash::launch_table_prep(t, st);
     if (int r = launch_status("table_prep")) return r;
+    if (verify)
+      return run_verify(S, vgu, vdn, RouteOut{}, inv_perm, workspace, L, gate_up, down, shared_gate_up, shared_down,
+                        out, st);
     return run_experts(S, inv_perm, workspace, L, gate_up, down, shared_gate_up, shared_down, out, st);
   } catch (...) {
     return fail(DFLASH_ERR_HIP, "unexpected host exception");
@@ -528,6 +730,10 @@ int dflash_moe_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, co
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int T = static_cast<int>(S.T), E = static_cast<int>(S.E);
     const bool small = dflash::route_small_fits(T, E, static_cast<int>(S.k));
+    // the verify path routes inside its gate/up launch when the block fits there
+    dflash::VerifyParams vgu, vdn;
+    const bool verify = tokens > 0 && small && verify_fits(S, true, &vgu, &vdn);
+    if (int r = check_tiled_moe(S, verify)) return r;
     float* logits = router_logits ? const_cast<float*>(router_logits)
                                   : (logits_out ? logits_out : at<float>(workspace, L.logits));
     dflash::FrontParams f{};
@@ -551,11 +757,16 @@ int dflash_moe_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, co
     }
     if (!measuring()) dflash::launch_front(f, st);
     if (int r = launch_status("front")) return r;
-    const dflash::RouteParams r = route_params(logits, S.T, S.E, S.k, topk_ids, topk_weights, perm, inv_perm,
-                                               expert_offsets, workspace, L.route, rows_per_pass(S), S.shared);
-    if (!measuring()) dflash::launch_route(r, true, st);
-    if (int rc = launch_status("route")) return rc;
+    if (!(verify && vgu.route)) {
+      const dflash::RouteParams r = route_params(logits, S.T, S.E, S.k, topk_ids, topk_weights, perm, inv_perm,
+                                                 expert_offsets, workspace, L.route, rows_per_pass(S), S.shared);
+      if (!measuring()) dflash::launch_route(r, true, st);
+      if (int rc = launch_status("route")) return rc;
+    }
     if (tokens == 0) return DFLASH_OK;
+    if (verify)
+      return run_verify(S, vgu, vdn, RouteOut{logits, topk_ids, topk_weights, perm, inv_perm, expert_offsets},
+                        inv_perm, workspace, L, gate_up, down, shared_gate_up, shared_down, out, st);
     return run_experts(S, inv_perm, workspace, L, gate_up, down, shared_gate_up, shared_down, out, st);
   } catch (...) {
     return fail(DFLASH_ERR_HIP, "unexpected host exception");

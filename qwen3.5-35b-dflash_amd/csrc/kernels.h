@@ -123,7 +123,12 @@ struct W4StreamParams {
   const float* slot_w;     // kModeDown: routing weight of every slot row [T*k]
   const float* shared_gate;// kModeDown: sigmoid gate [T]
   int M;                   // kModeLinear rows
+  int tiled;               // banks in the tiled layout (DFLASH_LAYOUT_TILED), else portable
 };
+
+// Portable -> tiled repack of a packed bank and its scales (repack.hip).
+void launch_tile_w4(const void* packed, const void* scales, bool fp32_scales, int64_t experts, int rows, int cols,
+                    int group, void* packed_out, void* scales_out, hipStream_t stream);
 
 void launch_front(const FrontParams& p, hipStream_t stream);
 // Router tiles of a launch: 32 tokens x 64 experts when T >= 64 and H % 128 == 0, else 16 x 16.
@@ -150,6 +155,36 @@ void launch_w4_stream(int mode, bool fp32_scales, int mt, int grid, const W4Stre
 bool w4_wave_supports(int mode, int K, int G, int rows);
 constexpr int kWaveMaxTokenRows = 2048;  // T * top_k routed slot rows whose tokens stay in LDS
 void launch_w4_wave(int mode, bool fp32_scales, int grid, const W4StreamParams& p, hipStream_t stream);
+// Verify-block expert kernels (w4_verify.hip), T <= 32 tokens: 16-row passes,
+// group 128, K in {512, 1024, 2048}.  Each workgroup splits its contiguous
+// range of units evenly over its 8 waves at k-block granularity; units split
+// between waves meet in LDS.  The gate/up launch can route in its prologue, so a
+// whole layer is front, gate/up, down, combine.
+struct VerifyParams {
+  W4StreamParams g;
+  // dynamic LDS layout, byte offsets (verify_layout)
+  int lds_a, lds_neg, lds_tok, lds_pdesc, lds_wgt, lds_part, lds_scratch, lds_bytes;
+  int pd_cap;        // pass descriptors the LDS holds
+  int a_rows;        // activation rows the LDS holds (gate/up: T; linear: M; down: chunk_passes * 16)
+  int chunk_passes;  // down: passes whose h rows are staged at once
+  // in-kernel routing (gate/up only): fp32 logits [T][E] -> the dflash_moe_route outputs
+  // (written by workgroup 0) and the work table of the down launch
+  int route, E;
+  const float* logits;
+  int32_t* ids;
+  float* wts;
+  int32_t* perm;
+  int32_t* inv;
+  int32_t* offsets;
+  int32_t* meta_out;       // [0] hit experts, [1] passes
+  int4* pass_table_out;
+  float* slot_w_out;
+  int32_t* tok_out;
+};
+// LDS bytes and layout of one verify launch; false when it does not fit (the
+// caller keeps the separate routing / wave-streaming kernels then).
+bool verify_layout(int mode, int T, int K, int N, int E, int k, int has_shared, int route, VerifyParams* vp);
+void launch_w4_verify(int mode, bool fp32_scales, int grid, const VerifyParams& vp, hipStream_t stream);
 // LDS-tiled kernel for long prefill (w4_tile.hip): 96-row passes, column tiles of 512
 // (p.strips = I / 256 for gate_up, H / 512 for down), K % 512 == 0; its gate_up writes one
 // -136*sum(h) per 128 columns and its down reads them that way.

@@ -17,7 +17,7 @@
 #include <algorithm>
 #include <utility>
 
-#include "kernels.h"
+#include "topk.h"
 
 namespace dflash {
 
@@ -25,86 +25,6 @@ namespace dflash {
 template <typename F, int... I>
 __device__ __forceinline__ void static_for(std::integer_sequence<int, I...>, F&& f) {
   (f(std::integral_constant<int, I>{}), ...);
-}
-
-// Order-preserving uint32 of a float: -0 folded to +0, NaN ranks below -inf.
-__device__ __forceinline__ uint32_t sortable_key(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0u;
-  if ((u & 0x7FFFFFFFu) == 0u) u = 0u;
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-__device__ __forceinline__ float key_to_float(uint32_t k) {
-  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
-}
-
-// Max of a 32-bit value over all 64 lanes, returned wave-uniform.
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-  auto dmax = [](uint32_t x, uint32_t y) { return x > y ? x : y; };
-  v = dmax(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xB1, 0xF, 0xF, false)));
-  v = dmax(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x4E, 0xF, 0xF, false)));
-  v = dmax(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x141, 0xF, 0xF, false)));
-  v = dmax(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x140, 0xF, 0xF, false)));
-  const uint32_t a = __builtin_amdgcn_readlane(static_cast<int>(v), 0), b = __builtin_amdgcn_readlane(static_cast<int>(v), 16);
-  const uint32_t c = __builtin_amdgcn_readlane(static_cast<int>(v), 32), d = __builtin_amdgcn_readlane(static_cast<int>(v), 48);
-  return dmax(dmax(a, b), dmax(c, d));
-}
-
-// Top-k of one token's logits by one wave.  Lane l holds experts l + 64 i as
-// 32-bit keys (sortable_key + 1; 0 marks padding and experts already taken).
-// Each of the k rounds takes the wave-wide maximum key, then the lowest
-// expert id holding it (a ballot per block of 64 ids, first set bit of the
-// first non-empty block): the larger logit wins and, among equal logits, the
-// lower expert id.  Lane s < k ends with (id_s, weight_s).
-template <int kPer>
-__device__ __forceinline__ void wave_topk(const float* __restrict__ row, int E, int k, int* id_out, float* w_out) {
-  const int lane = lane_id();
-  uint32_t key[kPer];
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int e = lane + 64 * i;
-    key[i] = e < E ? sortable_key(row[e]) + 1u : 0u;  // sortable keys stay below 0xFF800001
-  }
-  int my_id = -1;
-  uint32_t my_key = 0;
-  for (int s = 0; s < k; ++s) {
-    uint32_t m = key[0];
-#pragma unroll
-    for (int i = 1; i < kPer; ++i) m = m > key[i] ? m : key[i];
-    m = wave_max_u32(m);
-    int e = -1;
-#pragma unroll
-    for (int i = kPer - 1; i >= 0; --i) {  // the lowest block with a hit decides
-      const uint64_t hits = __ballot(key[i] == m);
-      if (hits) e = 64 * i + __builtin_ctzll(hits);
-    }
-    e = __builtin_amdgcn_readfirstlane(e);
-#pragma unroll
-    for (int i = 0; i < kPer; ++i)
-      if (lane + 64 * i == e) key[i] = 0u;
-    if (lane == s) {
-      my_id = e;
-      my_key = m - 1u;
-    }
-  }
-  const float top = key_to_float(__builtin_amdgcn_readlane(static_cast<int>(my_key), 0));
-  const float ex = (lane < k) ? expf(key_to_float(my_key) - top) : 0.f;
-  const float total = wave_sum(ex);
-  *id_out = my_id;
-  *w_out = ex / total;
-}
-
-__device__ __forceinline__ void topk_any(const float* row, int E, int k, int* id, float* w) {
-  if (E <= 64) wave_topk<1>(row, E, k, id, w);
-  else if (E <= 128) wave_topk<2>(row, E, k, id, w);
-  else if (E <= 256) wave_topk<4>(row, E, k, id, w);
-  else if (E <= 512) wave_topk<8>(row, E, k, id, w);
-  else wave_topk<16>(row, E, k, id, w);
-}
-
-__device__ __forceinline__ int passes_for(int rows, int rows_per_pass) {
-  return (rows + rows_per_pass - 1) / rows_per_pass;
 }
 
 // ---------------------------------------------------------------------------

@@ -42,19 +42,18 @@ struct WeightBuf {
   uint32_t s[2][kScaleWords];
 };
 
-// The wave's kKBPW consecutive group scales of one weight row (group 128).
+// The wave's kKBPW group scales (group 128) of one weight row: element kb at
+// src[kb * stride] (stride 1 in portable rows, 16 in the tiled layout); bf16
+// pairs share one word, k-block 0 in the low half.
 template <int kKBPW, typename ScaleT>
-__device__ __forceinline__ void load_scales(uint32_t* dst, const ScaleT* src) {
+__device__ __forceinline__ void load_scales(uint32_t* dst, const ScaleT* src, int stride) {
   if constexpr (sizeof(ScaleT) == 2 && kKBPW == 2) {
-    dst[0] = *reinterpret_cast<const uint32_t*>(src);
-  } else if constexpr (sizeof(ScaleT) == 2) {
-    dst[0] = *reinterpret_cast<const uint16_t*>(src);
+    dst[0] = load_scale_bits(src) | (load_scale_bits(src + stride) << 16);
   } else if constexpr (kKBPW == 2) {
-    const uint2 v = *reinterpret_cast<const uint2*>(src);
-    dst[0] = v.x;
-    dst[1] = v.y;
+    dst[0] = load_scale_bits(src);
+    dst[1] = load_scale_bits(src + stride);
   } else {
-    dst[0] = *reinterpret_cast<const uint32_t*>(src);
+    dst[0] = load_scale_bits(src);
   }
 }
 
@@ -233,8 +232,14 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(W4StreamParams p) {
   const int64_t w_second = second * rb, s_second = second * nkb;
   const int64_t w_strip = strip_rows * rb, s_strip = static_cast<int64_t>(strip_rows) * nkb;
   const int64_t w_first = rg * kTileRows * rb, s_first = static_cast<int64_t>(rg) * kTileRows * nkb;
-  const uint32_t wlane = static_cast<uint32_t>(lr * (p.K >> 1) + ks * kKBPW * 64 + kq * 16);
-  const uint32_t slane = static_cast<uint32_t>((lr * nkb + ks * kKBPW) * static_cast<int>(sizeof(ScaleT)));
+  // lane offsets and k-block strides: portable rows, or the tiled layout's kilobyte per
+  // 16-row tile and k-block (scales [tile][group][16]); tile bases agree in both
+  const uint32_t wkb = p.tiled ? 1024u : 64u;
+  const uint32_t wlane = p.tiled ? static_cast<uint32_t>(lane * 16 + ks * kKBPW * 1024)
+                                 : static_cast<uint32_t>(lr * (p.K >> 1) + ks * kKBPW * 64 + kq * 16);
+  const int skb = p.tiled ? 16 : 1;
+  const uint32_t slane = static_cast<uint32_t>((p.tiled ? ks * kKBPW * 16 + lr : lr * nkb + ks * kKBPW) *
+                                               static_cast<int>(sizeof(ScaleT)));
 
   // ---- load stream: uniform cursor and row pointers (tile 0 of the wave's row group)
   int l_u = u_begin;
@@ -257,11 +262,11 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(W4StreamParams p) {
   auto issue = [&](WeightBuf<kKBPW, ScaleT>& b) {
 #pragma unroll
     for (int kb = 0; kb < kKBPW; ++kb) {
-      b.w[0][kb] = *reinterpret_cast<const uint4*>(l_w + wlane + kb * 64);
-      b.w[1][kb] = *reinterpret_cast<const uint4*>(l_w + w_second + wlane + kb * 64);
+      b.w[0][kb] = *reinterpret_cast<const uint4*>(l_w + wlane + kb * wkb);
+      b.w[1][kb] = *reinterpret_cast<const uint4*>(l_w + w_second + wlane + kb * wkb);
     }
-    load_scales<kKBPW, ScaleT>(b.s[0], reinterpret_cast<const ScaleT*>(l_s + slane));
-    load_scales<kKBPW, ScaleT>(b.s[1], reinterpret_cast<const ScaleT*>(l_s + s_second * sizeof(ScaleT) + slane));
+    load_scales<kKBPW, ScaleT>(b.s[0], reinterpret_cast<const ScaleT*>(l_s + slane), skb);
+    load_scales<kKBPW, ScaleT>(b.s[1], reinterpret_cast<const ScaleT*>(l_s + s_second * sizeof(ScaleT) + slane), skb);
     // advance to the next unit of the range (the last one repeats: padding loads)
     if (l_u + 1 < u_end) {
       ++l_u;

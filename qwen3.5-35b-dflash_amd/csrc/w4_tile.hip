@@ -65,6 +65,7 @@ struct TileCtx {
   int rows, nt;
   buf_rsrc wrs, srs, ars, nrs;  // the slot's weights and scales, activations, their -136*sum terms
   uint32_t woff[4];         // byte offset of this lane's 16 bytes of each weight fragment (k-block 0)
+  uint32_t wkb;             // k-block stride of the weights: 64 (portable rows) or 1024 (tiled blocks)
   uint32_t soff;            // byte offset of the scale row this lane loads (fragment lane >> 4, column lane & 15)
   uint32_t aoff[3];         // byte offset of this lane's 16 bytes of activation blocks wave, wave + 8, wave + 16
   uint32_t noff;            // byte offset of the -136*sum terms of row 64 * wave + lane
@@ -129,9 +130,12 @@ __device__ __forceinline__ void tile_pass(const W4StreamParams& p, const TileLds
   auto load_w = [&](int kb, auto sw) {
     kb = min(kb, nkb - 1);
 #pragma unroll
-    for (int f = 0; f < 4; ++f) dma16(c.wrs, lds.w[sw] + (wave * 4 + f) * 64, c.woff[f], kb * 64);
+    for (int f = 0; f < 4; ++f) dma16(c.wrs, lds.w[sw] + (wave * 4 + f) * 64, c.woff[f], kb * c.wkb);
     const int g = kb >> gshift;
-    dma4(c.srs, lds.s[sw] + wave * 64, c.soff, sizeof(ScaleT) == 4 ? g * 4 : (g & ~1) * 2);
+    // portable: the 4 bytes at the lane's row and group (pair); tiled: the group's 16-column
+    // chunk at the lane's even column (a bf16 lane takes its half below)
+    dma4(c.srs, lds.s[sw] + wave * 64, c.soff,
+         p.tiled ? g * 16 * static_cast<int>(sizeof(ScaleT)) : (sizeof(ScaleT) == 4 ? g * 4 : (g & ~1) * 2));
   };
   // this lane's weights and group scales of k-block kb from stage sw
   auto read_w = [&](uint4 (&wf)[4], float (&sc)[4], int kb, auto sw) {
@@ -140,7 +144,8 @@ __device__ __forceinline__ void tile_pass(const W4StreamParams& p, const TileLds
     for (int f = 0; f < 4; ++f) {
       wf[f] = lds.w[sw][(wave * 4 + f) * 64 + lane];
       const uint32_t bits = lds.s[sw][wave * 64 + f * 16 + lr];
-      float v = sizeof(ScaleT) == 4 ? __uint_as_float(bits) : __uint_as_float((g & 1 ? bits >> 16 : bits & 0xFFFFu) << 16);
+      const bool hi = p.tiled ? (lr & 1) : (g & 1);
+      float v = sizeof(ScaleT) == 4 ? __uint_as_float(bits) : __uint_as_float((hi ? bits >> 16 : bits & 0xFFFFu) << 16);
       if (__builtin_fabsf(v) < 0x1p-64f) v = __builtin_copysignf(0x1p-64f, v);  // NaN passes through
       sc[f] = v;
     }
@@ -310,9 +315,15 @@ __device__ __forceinline__ void run_tile(const W4StreamParams& p, const TileLds&
   c.srs = make_rsrc(static_cast<const uint8_t*>(c.shared ? p.s_shared : p.s) +
                         (c.shared ? 0 : static_cast<int64_t>(c.d.x) * p.s_stride * static_cast<int64_t>(sizeof(ScaleT))),
                     static_cast<uint32_t>(p.N) * static_cast<uint32_t>(ng) * sizeof(ScaleT));
+  // a fragment's 16 rows are one tile of the tiled layout (its base is the same in both layouts)
+  c.wkb = p.tiled ? 1024u : 64u;
 #pragma unroll
-  for (int f = 0; f < 4; ++f) c.woff[f] = static_cast<uint32_t>(wrow(f, lr)) * rb + kq * 16;
-  c.soff = static_cast<uint32_t>(wrow(lane >> 4, lr)) * static_cast<uint32_t>(ng) * sizeof(ScaleT);
+  for (int f = 0; f < 4; ++f)
+    c.woff[f] = p.tiled ? static_cast<uint32_t>(wrow(f, 0)) * rb + lane * 16
+                        : static_cast<uint32_t>(wrow(f, lr)) * rb + kq * 16;
+  c.soff = p.tiled ? (static_cast<uint32_t>(wrow(lane >> 4, 0)) * static_cast<uint32_t>(ng) +
+                      static_cast<uint32_t>(sizeof(ScaleT) == 4 ? lr : lr & ~1)) * sizeof(ScaleT)
+                   : static_cast<uint32_t>(wrow(lane >> 4, lr)) * static_cast<uint32_t>(ng) * sizeof(ScaleT);
 
   // source row of pass row r (rows past the pass repeat its last row)
   auto src_row = [&](int r) {

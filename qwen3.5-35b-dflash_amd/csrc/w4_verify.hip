@@ -1,0 +1,588 @@
+// Verify-block W4A16 expert GEMMs (T <= 32 tokens): the routed-MoE layer of a
+// DFlash verify block in four launches (router front, gate/up, down, combine).
+//
+// Work decomposition.  A unit is one pass (up to 16 slot rows of an expert
+// segment or of the shared expert) times one strip of 2 x 16 weight rows over
+// the full reduction length K.  Units form one list (pass-major); each
+// workgroup takes an equal contiguous range of it, and inside the workgroup the
+// range's k-blocks (128 columns of K) are split evenly over the 8 waves at
+// multiples of 4 k-blocks, so every wave streams the same number of weight
+// bytes whatever the unit count.  A unit whose k-blocks fall to several waves
+// is finished by the wave holding its last k-block, after the others left their
+// partial sums in LDS (summed in wave order: the result does not depend on
+// timing).
+//
+// Per k-block a lane issues two 16-byte weight loads (16 rows x 64 bytes per
+// tile), 3 k-blocks ahead of the one it computes; a unit's group scales ride
+// with its first k-block (16-byte loads of whole scale rows).  Each k-block is
+// dequantised in registers (bf16 136+q), multiplied on
+// v_mfma_f32_16x16x32_bf16 against A fragments read from LDS, started from
+// -136*sum(a) and scaled.
+//
+// Prologues and epilogues:
+//   gate/up : optionally routes the block itself (top-k of the fp32 logits per
+//             token, counts, scans and the stable permutation in LDS: every
+//             workgroup derives the same work list, workgroup 0 also writes the
+//             routing outputs and the down launch's work table), stages x,
+//             its -136*sum terms and the token of every slot row in LDS; the
+//             epilogue writes h = silu(g)*u in bf16 and its -136*sum per 16
+//             columns.
+//   down    : stages the h rows of its passes (chunks that fit in LDS); the
+//             epilogue writes y = route_weight * (h . Wd^T) in fp32, which the
+//             combine kernel sums over slots.  (Combining inside this launch
+//             would need an agent-scope release per workgroup, an L2 write-back
+//             on every XCD, which measured slower than one more launch.)
+//   linear  : x rows of a plain qlinear (one pass per 16 rows).
+//
+// Semantics per mode (reference citations):
+//   kModeLinear : y = x . dequant(W)^T, bf16 out                 (fused/quantization.py:154-165)
+//   kModeGateUp : h = silu(x.Wg^T) * (x.Wu^T), gate rows first   (reference/fused_ops.py:170-171)
+//   kModeDown   : y = route_weight * (h . Wd^T), fp32            (fused/quantization.py:196-199)
+//   routing     : top-k, renormalised softmax, stable permutation (reference/fused_ops.py:160-164,
+//                                                                   fused/quantization.py:184-191)
+#include <algorithm>
+
+#include "topk.h"
+
+namespace dflash {
+namespace {
+
+constexpr int kVWaves = 8;
+constexpr int kVThreads = kVWaves * 64;
+constexpr int kVDepthAll = 3;    // k-blocks per wave in flight (loads run 2 ahead, across units)
+constexpr int kVStrip = 32;      // output columns per down/linear unit (and per combine strip)
+constexpr int kVLds = 158 * 1024;  // one persistent workgroup per CU
+
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+__device__ __forceinline__ void dma16(buf_rsrc r, void* dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)dst, 16, static_cast<int>(voff), static_cast<int>(soff), 0, 0);
+}
+__device__ __forceinline__ void dma4(buf_rsrc r, void* dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)dst, 4, static_cast<int>(voff), static_cast<int>(soff), 0, 0);
+}
+
+// Opaque to the optimiser: the value must exist in registers at this point.
+__device__ __forceinline__ void pin(f32x4& v) { asm volatile("" : "+v"(v)); }
+
+// ---------------------------------------------------------------------------
+// In-kernel routing of the block (512 threads, T <= 32, E <= 1024).  Leaves
+// every pass descriptor in pdesc and the token of every slot row in tok;
+// returns the number of passes.  Workgroup 0 writes the routing outputs
+// (ids, weights, perm, inv, offsets) and the work table the down launch reads.
+__device__ int route_block(const VerifyParams& vp, char* lds, int4* pdesc, int* tok) {
+  const int T = vp.g.T, E = vp.E, k = vp.g.top_k;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id();
+  const int tpad = (T + 3) & ~3;
+  const int epad = (E + 3) & ~3;
+  const bool out = blockIdx.x == 0;
+  int* cnt = reinterpret_cast<int*>(lds + vp.lds_scratch);   // [epad]
+  float* rw = reinterpret_cast<float*>(cnt + epad);          // [T*k]
+  int* wtot = reinterpret_cast<int*>(rw + ((T * k + 3) & ~3));  // [3][8]
+  uint32_t* map_words = reinterpret_cast<uint32_t*>(wtot + 24);  // [E][tpad] bytes
+  uint8_t* map = reinterpret_cast<uint8_t*>(map_words);
+  for (int i = tid; i < epad; i += kVThreads) cnt[i] = 0;
+  for (int i = tid; i < (E * tpad) / 4; i += kVThreads) map_words[i] = 0u;
+  __syncthreads();
+  // tokens 2 * wave + {0, 1} (+ 16 for T > 16), two per wave at a time
+  for (int t0 = 2 * wave; t0 < T; t0 += 2 * kVWaves) {
+    const bool live_b = t0 + 1 < T;
+    int id[2];
+    float w[2];
+    topk2_any(vp.logits + static_cast<int64_t>(t0) * E, vp.logits + static_cast<int64_t>(live_b ? t0 + 1 : t0) * E,
+              live_b, E, k, id, w);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int t = t0 + r;
+      if (lane < k && (r == 0 || live_b)) {
+        rw[t * k + lane] = w[r];
+        atomicAdd(&cnt[id[r]], 1);
+        map[id[r] * tpad + t] = static_cast<uint8_t>(lane + 1);
+        if (out) {
+          vp.ids[t * k + lane] = id[r];
+          vp.wts[t * k + lane] = w[r];
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // exclusive scans over experts (two per thread): segment start, hit index, first pass
+  int c[2], np[2], a = 0, b = 0, pc = 0;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int e = 2 * tid + j;
+    c[j] = e < E ? cnt[e] : 0;
+    np[j] = passes_for(c[j], 16);
+    a += c[j];
+    b += c[j] > 0 ? 1 : 0;
+    pc += np[j];
+  }
+  int ia = a, ib = b, ic = pc;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int ua = __shfl_up(ia, o, 64), ub = __shfl_up(ib, o, 64), uc = __shfl_up(ic, o, 64);
+    if (lane >= o) {
+      ia += ua;
+      ib += ub;
+      ic += uc;
+    }
+  }
+  if (lane == 63) {
+    wtot[wave] = ia;
+    wtot[8 + wave] = ib;
+    wtot[16 + wave] = ic;
+  }
+  __syncthreads();
+  int ba = 0, bb = 0, bc = 0, hits = 0, routed = 0;
+#pragma unroll
+  for (int i = 0; i < kVWaves; ++i) {
+    const int va = wtot[i], vb = wtot[8 + i], vc = wtot[16 + i];
+    if (i < wave) {
+      ba += va;
+      bb += vb;
+      bc += vc;
+    }
+    hits += vb;
+    routed += vc;
+  }
+  int off = ba + ia - a, pass = bc + ic - pc;
+  (void)bb;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int e = 2 * tid + j;
+    if (e < E) {
+      if (out) vp.offsets[e] = off;
+      for (int i = 0; i < np[j]; ++i) {
+        const int4 d = make_int4(e, off, c[j], 16 * i);
+        pdesc[pass + i] = d;
+        if (out) vp.pass_table_out[pass + i] = d;
+      }
+    }
+    off += c[j];
+    pass += np[j];
+  }
+  const int shared_passes = vp.g.has_shared ? passes_for(T, 16) : 0;
+  if (tid < shared_passes) {
+    const int4 d = make_int4(-1, 0, T, 16 * tid);
+    pdesc[routed + tid] = d;
+    if (out) vp.pass_table_out[routed + tid] = d;
+  }
+  if (out && tid == 0) {
+    vp.offsets[E] = T * k;
+    vp.meta_out[0] = hits;
+    vp.meta_out[1] = routed + shared_passes;
+  }
+  // stable ranks: the thread of expert e walks its slot-map row (tokens ascending)
+  off = ba + ia - a;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int e = 2 * tid + j;
+    if (c[j] > 0) {
+      int pos = off;
+      const uint32_t* row = map_words + (e * tpad) / 4;
+      for (int q = 0; q < tpad / 4; ++q) {
+        uint32_t word = row[q];
+        while (word) {
+          const int byte = __builtin_ctz(word) >> 3;
+          const int t = q * 4 + byte;
+          const int flat = t * k + static_cast<int>((word >> (byte * 8)) & 0xFFu) - 1;
+          tok[pos] = t;
+          if (out) {
+            vp.perm[pos] = flat;
+            vp.inv[flat] = pos;
+            vp.slot_w_out[pos] = rw[flat];
+            vp.tok_out[pos] = t;
+          }
+          ++pos;
+          word &= ~(0xFFu << (byte * 8));
+        }
+      }
+    }
+    off += c[j];
+  }
+  __syncthreads();
+  return routed + shared_passes;
+}
+
+}  // namespace
+
+template <int kMode, int kNKB, typename ScaleT>
+__global__ __launch_bounds__(512) void w4_verify_kernel(VerifyParams vp) {
+  __shared__ __attribute__((aligned(16))) char lds[kVLds];
+  const W4StreamParams& p = vp.g;
+  constexpr int kK = kNKB * 128;
+  constexpr int kRS = kK * 2 + 16;                  // LDS row stride (bytes) of an activation row
+  constexpr int kTileRows = kMode == kModeGateUp ? 16 : 32;
+  constexpr int kVDepth = kVDepthAll;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = lane_id(), lr = lane & 15, kq = lane >> 4;
+  const int tid = threadIdx.x;
+
+  uint8_t* lds_a = reinterpret_cast<uint8_t*>(lds + vp.lds_a);
+  float* lds_neg = reinterpret_cast<float*>(lds + vp.lds_neg);
+  int* lds_tok = reinterpret_cast<int*>(lds + vp.lds_tok);
+  int4* lds_pdesc = reinterpret_cast<int4*>(lds + vp.lds_pdesc);
+  float* lds_wgt = reinterpret_cast<float*>(lds + vp.lds_wgt);
+  f32x4* lds_part = reinterpret_cast<f32x4*>(lds + vp.lds_part);  // [wave][2][64]
+
+  // ---- passes of the launch
+  int total_passes;
+  if (kMode == kModeGateUp && vp.route) {
+    total_passes = route_block(vp, lds, lds_pdesc, lds_tok);
+  } else if (kMode == kModeLinear) {
+    total_passes = (p.M + 15) >> 4;
+  } else {
+    total_passes = ld_const(p.meta, 1);
+  }
+  const int strips = p.strips;
+  const int64_t total_units = static_cast<int64_t>(total_passes) * strips;
+  const int ub = static_cast<int>(total_units * blockIdx.x / gridDim.x);
+  const int ue = static_cast<int>(total_units * (blockIdx.x + 1) / gridDim.x);
+
+  const int64_t rb = kK >> 1;                                      // packed bytes per weight row
+  const int64_t second = kMode == kModeGateUp ? (p.N >> 1) : 16;   // row distance of tile 1
+  // lane offset inside a 16-row tile and k-block stride: portable rows, or the tiled
+  // layout's contiguous kilobyte per k-block (tile bases are the same in both)
+  const uint32_t wlane = p.tiled ? static_cast<uint32_t>(lane * 16) : static_cast<uint32_t>(lr * rb + kq * 16);
+  const uint32_t wkb = p.tiled ? 1024u : 64u;
+  const int slane = p.tiled ? lr : lr * kNKB;  // scale elements: [tile][group][16] or [row][group]
+  const int skb = p.tiled ? 16 : 1;
+
+  const int P_first = ub / strips, P_last = ue > ub ? (ue - 1) / strips : P_first - 1;
+  // pass descriptors: all of them after in-kernel routing, else the chunk's (staged below)
+  int pd_base = 0;
+  auto pass_desc = [&](int P) -> int4 {
+    if (kMode == kModeLinear) return make_int4(0, 0, p.M, P * 16);
+    const int4 v = lds_pdesc[P - pd_base];
+    return make_int4(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
+                     __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w));
+  };
+
+  const int chunk_passes = kMode == kModeDown ? vp.chunk_passes : max(P_last - P_first + 1, 1);
+  for (int Pc = P_first; Pc <= P_last; Pc += chunk_passes) {
+    const int Pc_end = min(P_last + 1, Pc + chunk_passes);
+    const int cb = max(ub, Pc * strips), ce = min(ue, Pc_end * strips);
+    if (Pc != P_first) __syncthreads();  // every wave is done with the previous chunk's rows
+
+    // ---- stage the chunk's activation rows and descriptors
+    if (kMode == kModeGateUp || kMode == kModeLinear) {
+      if (!(kMode == kModeGateUp && vp.route)) {
+        pd_base = Pc;
+        if (kMode == kModeGateUp)
+          for (int i = tid; i < Pc_end - Pc; i += kVThreads) lds_pdesc[i] = p.pass_table[Pc + i];
+      }
+      // x rows: 1 KB blocks by direct-to-LDS loads; the -136*sum terms; the token of every slot row
+      const int rows = kMode == kModeLinear ? p.M : p.T;
+      const buf_rsrc xr = make_rsrc(p.act, static_cast<uint32_t>(rows) * kK * 2);
+      constexpr int kBlk = kK / 512;  // 1 KB blocks per row
+      for (int i = wave; i < rows * kBlk; i += kVWaves) {
+        const int r = i / kBlk, bl = i - r * kBlk;
+        dma16(xr, lds_a + r * kRS + bl * 1024, static_cast<uint32_t>(lane * 16), static_cast<uint32_t>((r * kK + bl * 512) * 2));
+      }
+      const buf_rsrc nr = make_rsrc(p.act_neg, static_cast<uint32_t>(rows) * kNKB * 4);
+      for (int i = wave; i * 64 < rows * kNKB; i += kVWaves)
+        dma4(nr, lds_neg + i * 64, static_cast<uint32_t>(lane * 4), static_cast<uint32_t>(i * 256));
+      if (kMode == kModeGateUp && !vp.route)
+        for (int i = tid; i < p.T * p.top_k; i += kVThreads) lds_tok[i] = p.tok[i];
+    } else {
+      // down: per pass of the chunk its 16 h rows (clamped to the slot), -136*sum terms
+      // (8 partials of 16 columns per k-block) and routing weights
+      pd_base = Pc;
+      const int npass = Pc_end - Pc;
+      for (int i = tid; i < npass; i += kVThreads) lds_pdesc[i] = p.pass_table[Pc + i];
+      const int hrows = p.T * p.top_k + (p.has_shared ? p.T : 0);
+      const buf_rsrc hr = make_rsrc(p.act, static_cast<uint32_t>(hrows) * kK * 2);
+      constexpr int kBlk = kK / 512;
+      for (int i = wave; i < npass * 16 * kBlk; i += kVWaves) {
+        const int rr = i / kBlk, bl = i - rr * kBlk;
+        const int4 d = ld_const_int4(p.pass_table, Pc + rr / 16);
+        const int base = d.x < 0 ? p.T * p.top_k : d.y;
+        const int row = base + min(d.w + (rr & 15), d.z - 1);
+        dma16(hr, lds_a + rr * kRS + bl * 1024, static_cast<uint32_t>(lane * 16),
+              static_cast<uint32_t>((row * kK + bl * 512) * 2));
+      }
+      for (int i = tid; i < npass * 16 * kNKB; i += kVThreads) {
+        const int rr = i / kNKB, kb = i - rr * kNKB;
+        const int4 d = p.pass_table[Pc + rr / 16];
+        const int base = d.x < 0 ? p.T * p.top_k : d.y;
+        const int row = base + min(d.w + (rr & 15), d.z - 1);
+        const float4* ns = reinterpret_cast<const float4*>(p.act_neg + (static_cast<int64_t>(row) * kNKB + kb) * 8);
+        const float4 u = ns[0], v = ns[1];
+        lds_neg[i] = ((u.x + u.y) + (u.z + u.w)) + ((v.x + v.y) + (v.z + v.w));
+      }
+      for (int i = tid; i < npass * 16; i += kVThreads) {
+        const int4 d = p.pass_table[Pc + i / 16];
+        const int m = min(d.w + (i & 15), d.z - 1);
+        lds_wgt[i] = d.x < 0 ? p.shared_gate[m] : p.slot_w[d.y + m];
+      }
+    }
+    wait_vmem();
+    __syncthreads();
+
+    // ---- this wave's k-blocks of the chunk: [g0, g1), an exact eighth of them
+    const int n = (ce - cb) * kNKB;
+    const int g0 = (n * wave) / kVWaves, g1 = (n * (wave + 1)) / kVWaves;
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+
+    // epilogue of unit ur (chunk-relative) from its complete sums
+    auto finish = [&](int ur, const int4& cd, const f32x4& t0, const f32x4& t1) {
+      const int u = cb + ur;
+      const int P = u / strips, strip = u - P * strips;
+      const int M = cd.z, m0 = cd.w;
+      const bool shared = kMode != kModeLinear && cd.x < 0;
+      const int row0 = strip * kTileRows;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = m0 + 4 * kq + e;
+        const bool valid = m < M;
+        if (kMode == kModeLinear) {
+          if (valid) {
+            uint16_t* o = p.out_bf16 + static_cast<int64_t>(m) * p.N + row0 + lr;
+            o[0] = f32_to_bf16(t0[e]);
+            o[16] = f32_to_bf16(t1[e]);
+          }
+        } else if (kMode == kModeGateUp) {
+          const int inter = p.N >> 1;
+          const uint16_t hb = f32_to_bf16(silu(t0[e]) * t1[e]);
+          const int hrow = shared ? p.T * p.top_k + m : cd.y + m;
+          if (valid) p.out_bf16[static_cast<int64_t>(hrow) * inter + octet_slot(row0 + lr)] = hb;
+          const float part = row16_sum(valid ? bf16_to_f32(hb) : 0.f);
+          if (valid && lr == 0) p.out_part[static_cast<int64_t>(hrow) * (inter >> 4) + strip] = -kDequantOffset * part;
+        } else {
+          if (valid) {
+            const float wg = lds_wgt[(P - Pc) * 16 + 4 * kq + e];
+            const int yrow = shared ? p.T * p.top_k + m : cd.y + m;
+            float* o = p.out_f32 + static_cast<int64_t>(yrow) * p.N + row0 + lr;
+            o[0] = t0[e] * wg;
+            o[16] = t1[e] * wg;
+          }
+        }
+      }
+    };
+
+    f32x4 head0 = zero, head1 = zero;
+    int head_unit = -1;  // chunk-relative unit this wave ends but did not begin
+    if (g0 < g1) {
+      // load cursor: next k-block to issue and the bases of its unit
+      int lg = g0, l_ur = -1;
+      const uint8_t* l_w = nullptr;
+      const uint8_t* l_s = nullptr;
+      auto unit_bases = [&](int ur) {
+        const int u = cb + ur;
+        const int P = u / strips, strip = u - P * strips;
+        const int4 d = pass_desc(P);
+        const bool shared = kMode != kModeLinear && d.x < 0;
+        const int64_t e = kMode == kModeLinear ? 0 : d.x;
+        const uint8_t* wbase = shared ? p.w_shared : p.w + e * p.w_stride;
+        const uint8_t* sbase = static_cast<const uint8_t*>(shared ? p.s_shared : p.s) +
+                               (shared ? 0 : e * p.s_stride * static_cast<int64_t>(sizeof(ScaleT)));
+        const int64_t row0 = static_cast<int64_t>(strip) * kTileRows;
+        l_w = wbase + row0 * rb;
+        l_s = sbase + row0 * kNKB * static_cast<int64_t>(sizeof(ScaleT));
+      };
+      // ring of k-blocks in flight: two 16-byte weight loads and the two group scales of the lane's rows
+      uint4 wbuf[kVDepth][2];
+      uint32_t sbuf[kVDepth][2];
+      // Loads are issued unconditionally (past the range they repeat its last k-block, never
+      // computed): a load under a branch would make the compiler drain the queue at the loop edge.
+      auto issue = [&](uint4 (&dst)[2], uint32_t (&sdst)[2]) {
+        const int lc = min(lg, g1 - 1);
+        const int ur = lc / kNKB, kb = lc - ur * kNKB;
+        if (ur != l_ur) {
+          l_ur = ur;
+          unit_bases(ur);
+        }
+        dst[0] = *reinterpret_cast<const uint4*>(l_w + wlane + kb * wkb);
+        dst[1] = *reinterpret_cast<const uint4*>(l_w + second * rb + wlane + kb * wkb);
+        const ScaleT* sp = reinterpret_cast<const ScaleT*>(l_s) + slane + kb * skb;
+        sdst[0] = load_scale_bits(sp);
+        sdst[1] = load_scale_bits(sp + second * kNKB);
+        ++lg;
+      };
+#pragma unroll
+      for (int i = 0; i + 1 < kVDepth; ++i) issue(wbuf[i], sbuf[i]);
+
+      // compute state of the current unit
+      int c_ur = -1, P = 0, a_off = 0;
+      int4 cd = make_int4(0, 0, 0, 0);
+      int n_idx[4] = {0, 0, 0, 0};
+      bool began = false;
+      f32x4 tot0 = zero, tot1 = zero;
+      for (int gs = g0; gs < g1; gs += kVDepth) {
+#pragma unroll
+        for (int i = 0; i < kVDepth; ++i) {
+          const int g = gs + i;
+          issue(wbuf[(i + kVDepth - 1) % kVDepth], sbuf[(i + kVDepth - 1) % kVDepth]);
+          if (g < g1) {
+            const int ur = g / kNKB, kb = g - ur * kNKB;
+            if (ur != c_ur) {
+              c_ur = ur;
+              const int u = cb + ur;
+              P = u / strips;
+              cd = pass_desc(P);
+              const int M = cd.z, m0 = cd.w;
+              const int ma = min(m0 + lr, M - 1);
+              int arow;
+              if (kMode == kModeGateUp) arow = cd.x < 0 ? ma : lds_tok[cd.y + ma];
+              else if (kMode == kModeLinear) arow = ma;
+              else arow = (P - Pc) * 16 + lr;
+              a_off = arow * kRS + kq * 64;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int me = min(m0 + 4 * kq + e, M - 1);
+                int nrow;
+                if (kMode == kModeGateUp) nrow = cd.x < 0 ? me : lds_tok[cd.y + me];
+                else if (kMode == kModeLinear) nrow = me;
+                else nrow = (P - Pc) * 16 + 4 * kq + e;
+                n_idx[e] = nrow * kNKB;
+              }
+              began = kb == 0;
+              tot0 = zero;
+              tot1 = zero;
+            }
+            const uint8_t* ab = lds_a + a_off + kb * 256;
+            uint4 a[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) a[j] = *reinterpret_cast<const uint4*>(ab + 16 * j);
+            const f32x4 start = {lds_neg[n_idx[0] + kb], lds_neg[n_idx[1] + kb], lds_neg[n_idx[2] + kb],
+                                 lds_neg[n_idx[3] + kb]};
+            const uint4 (&w)[2] = wbuf[i];
+            const uint32_t w0[4] = {w[0].x, w[0].y, w[0].z, w[0].w};
+            const uint32_t w1[4] = {w[1].x, w[1].y, w[1].z, w[1].w};
+            f32x4 acc0 = start, acc1 = start;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              acc0 = mfma16x16x32(a[j], dequant8(w0[j]), acc0);
+              acc1 = mfma16x16x32(a[j], dequant8(w1[j]), acc1);
+            }
+            tot0 += scale_value<ScaleT>(sbuf[i][0]) * acc0;
+            tot1 += scale_value<ScaleT>(sbuf[i][1]) * acc1;
+            // materialise the running sums here: left alone, the compiler sinks the
+            // scale-accumulates and keeps every k-block's MFMA result live
+            pin(tot0);
+            pin(tot1);
+            if (kb == kNKB - 1) {
+              if (began) {
+                finish(ur, cd, tot0, tot1);
+              } else {
+                // this wave ends a unit others began: finish it once their partials are in
+                head0 = tot0;
+                head1 = tot1;
+                head_unit = ur;
+              }
+            } else if (g == g1 - 1) {
+              // the unit continues in the next wave: leave the partial sums
+              lds_part[(wave * 2) * 64 + lane] = tot0;
+              lds_part[(wave * 2 + 1) * 64 + lane] = tot1;
+            }
+          }
+          // keep the scheduler from hoisting later k-blocks' LDS reads and
+          // dequantisation into this one (register pressure, not latency, binds)
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+    __syncthreads();  // partial sums of split units are in LDS
+    if (head_unit >= 0) {
+      // sum the partials of the waves before this one that share the unit, in wave order
+      const int gs = head_unit * kNKB;
+      int wa = wave - 1;
+      while (wa > 0 && (n * wa) / kVWaves > gs) --wa;
+      f32x4 t0 = zero, t1 = zero;
+      for (int w = wa; w < wave; ++w) {
+        if ((n * w) / kVWaves < (n * (w + 1)) / kVWaves) {
+          t0 += lds_part[(w * 2) * 64 + lane];
+          t1 += lds_part[(w * 2 + 1) * 64 + lane];
+        }
+      }
+      t0 += head0;
+      t1 += head1;
+      finish(head_unit, pass_desc((cb + head_unit) / strips), t0, t1);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+bool verify_layout(int mode, int T, int K, int N, int E, int k, int has_shared, int route, VerifyParams* vp) {
+  if (K != 512 && K != 1024 && K != 2048) return false;
+  if (T <= 0 || T > 32 || k <= 0) return false;
+  if (N % (mode == kModeGateUp ? 32 : kVStrip)) return false;
+  const int rs = 2 * K + 16, nkb = K / 128;
+  auto al = [](int v) { return (v + 15) & ~15; };
+  const int part = kVWaves * 2 * 64 * 16;
+  int off = 0;
+  auto take = [&](int bytes) {
+    const int o = off;
+    off += al(bytes);
+    return o;
+  };
+  VerifyParams& L = *vp;
+  L.route = 0;
+  if (mode == kModeDown) {
+    const int per_pass = 16 * rs + al(16 * nkb * 4) + al(16 * 4) + 16;
+    const int fixed = part;
+    const int cp = std::min(8, (kVLds - fixed) / per_pass);
+    if (cp < 1) return false;
+    L.chunk_passes = cp;
+    L.pd_cap = cp;
+    L.a_rows = cp * 16;
+    L.lds_a = take(cp * 16 * rs);
+    L.lds_neg = take(cp * 16 * nkb * 4);
+    L.lds_wgt = take(cp * 16 * 4);
+    L.lds_pdesc = take(cp * 16);
+    L.lds_tok = 0;
+    L.lds_part = L.lds_scratch = take(part);
+    L.lds_bytes = off;
+    return off <= kVLds;
+  }
+  L.chunk_passes = 0;
+  L.a_rows = T;
+  L.lds_a = take(T * rs);
+  L.lds_neg = take(((T * nkb + 63) & ~63) * 4);  // filled 64 terms per direct-to-LDS load
+  L.lds_wgt = 0;
+  if (mode == kModeLinear) {
+    L.pd_cap = 0;
+    L.lds_tok = L.lds_pdesc = 0;
+    L.lds_part = L.lds_scratch = take(part);
+    L.lds_bytes = off;
+    return off <= kVLds;
+  }
+  const int tpasses = (T + 15) / 16;
+  L.pd_cap = std::min(E, T * k) * tpasses + (has_shared ? tpasses : 0);
+  L.lds_tok = take(T * k * 4);
+  L.lds_pdesc = take(L.pd_cap * 16);
+  const int base = off;
+  const int scratch = al(((E + 3) & ~3) * 4) + al(((T * k + 3) & ~3) * 4) + 96 + E * ((T + 3) & ~3);
+  if (route && E <= 2 * kVThreads && base + std::max(part, al(scratch)) <= kVLds) {
+    L.route = 1;
+    L.lds_part = L.lds_scratch = take(std::max(part, scratch));
+  } else {
+    L.lds_part = L.lds_scratch = take(part);
+  }
+  L.lds_bytes = off;
+  return off <= kVLds;
+}
+
+void launch_w4_verify(int mode, bool fp32_scales, int grid, const VerifyParams& vp, hipStream_t stream) {
+  const dim3 g(static_cast<unsigned>(grid)), blk(kVThreads);
+#define DFLASH_VERIFY(MODE, NKB)                                                                           \
+  do {                                                                                                     \
+    if (fp32_scales) hipLaunchKernelGGL((w4_verify_kernel<MODE, NKB, float>), g, blk, 0, stream, vp);     \
+    else hipLaunchKernelGGL((w4_verify_kernel<MODE, NKB, uint16_t>), g, blk, 0, stream, vp);              \
+  } while (0)
+#define DFLASH_VERIFY_K(MODE)                    \
+  switch (vp.g.K) {                              \
+    case 512: DFLASH_VERIFY(MODE, 4); break;     \
+    case 1024: DFLASH_VERIFY(MODE, 8); break;    \
+    default: DFLASH_VERIFY(MODE, 16); break;     \
+  }
+  switch (mode) {
+    case kModeLinear: DFLASH_VERIFY_K(kModeLinear) break;
+    case kModeGateUp: DFLASH_VERIFY_K(kModeGateUp) break;
+    default: DFLASH_VERIFY_K(kModeDown) break;
+  }
+#undef DFLASH_VERIFY_K
+#undef DFLASH_VERIFY
+}
+
+}  // namespace dflash

@@ -55,7 +55,8 @@ def _desc(w: PackedW4) -> _lib.W4Desc:
     return _lib.W4Desc(
         packed=w.packed.data_ptr(), scales=w.scales.data_ptr(), experts=w.experts, rows=w.rows, cols=w.cols,
         group_size=w.group_size,
-        scale_dtype=_lib.DTYPE_F32 if w.scales.dtype == torch.float32 else _lib.DTYPE_BF16)
+        scale_dtype=_lib.DTYPE_F32 if w.scales.dtype == torch.float32 else _lib.DTYPE_BF16,
+        layout=_lib.LAYOUT_TILED if w.layout == "tiled" else _lib.LAYOUT_PORTABLE)
 
 
 def _workspace(nbytes: int, device: torch.device, workspace: Optional[torch.Tensor]) -> torch.Tensor:
@@ -64,6 +65,19 @@ def _workspace(nbytes: int, device: torch.device, workspace: Optional[torch.Tens
             raise ValueError(f"workspace must be a uint8 tensor of at least {nbytes} bytes on {device}")
         return workspace
     return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+
+
+def to_tiled(w: PackedW4) -> PackedW4:
+    """Repack a portable bank into the tiled layout (new tensors, same shapes, on w's device)."""
+    w.validate("weight")
+    if w.layout != "portable":
+        raise ValueError("to_tiled needs a portable bank")
+    device = _require_device(w.packed)
+    packed = torch.empty_like(w.packed)
+    scales = torch.empty_like(w.scales)
+    desc = _desc(w)
+    _lib.call("dflash_w4_to_tiled", ctypes.byref(desc), _ptr(packed), _ptr(scales), _stream(device))
+    return PackedW4(packed, scales, w.group_size, "tiled")
 
 
 def qlinear(x: torch.Tensor, weight: PackedW4, *, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:

@@ -7,6 +7,13 @@ nibble of byte ``j``; scales are ``[..., N, K/G]`` (bf16 or fp32) and the
 dequantised weight is ``q * scale[k // G]``.  The reference fixes ``G = 256``
 and fp32 scales; here ``G`` is 128 or 256 and bf16 scales are accepted too
 (W4A16 plan, ``reference/quantization.py:87-89``).
+
+A bank may also be held in the *tiled* layout (``layout="tiled"``, made once by
+``PackedW4.tiled()`` on the device): the same bytes and scales permuted so that
+each 16-row tile and 128-column block is one contiguous kilobyte in the order
+the expert kernels' 64 lanes load it, and scales are ``[..., N/16, K/G, 16]``
+(byte-exact definition in ``include/dflash_hip.h``).  Tensor shapes are those
+of the portable layout; only the order of the bytes differs.
 """
 from __future__ import annotations
 
@@ -15,6 +22,7 @@ from typing import NamedTuple
 import torch
 
 GROUP_SIZES = (128, 256)
+LAYOUTS = ("portable", "tiled")
 
 
 class PackedW4(NamedTuple):
@@ -23,6 +31,7 @@ class PackedW4(NamedTuple):
     packed: torch.Tensor
     scales: torch.Tensor
     group_size: int
+    layout: str = "portable"
 
     @property
     def experts(self) -> int:
@@ -53,9 +62,18 @@ class PackedW4(NamedTuple):
             raise ValueError(f"{name}: packed and scales on different devices")
         if not p.is_contiguous() or not s.is_contiguous():
             raise ValueError(f"{name}: packed and scales must be contiguous")
+        if self.layout not in LAYOUTS:
+            raise ValueError(f"{name}: layout must be one of {LAYOUTS}")
+        if self.layout == "tiled" and (p.shape[-2] % 16 or k % 128):
+            raise ValueError(f"{name}: the tiled layout needs N % 16 == 0 and K % 128 == 0")
 
     def to(self, device) -> "PackedW4":
-        return PackedW4(self.packed.to(device), self.scales.to(device), self.group_size)
+        return PackedW4(self.packed.to(device), self.scales.to(device), self.group_size, self.layout)
+
+    def tiled(self) -> "PackedW4":
+        """This bank in the tiled layout (a one-time repack on its ROCm device)."""
+        from .ops import to_tiled
+        return to_tiled(self)
 
 
 class SharedExpert(NamedTuple):
@@ -68,6 +86,10 @@ class SharedExpert(NamedTuple):
     gate_up: PackedW4
     down: PackedW4
     gate_weight: torch.Tensor
+
+    def tiled(self) -> "SharedExpert":
+        """Both banks in the tiled layout."""
+        return SharedExpert(self.gate_up.tiled(), self.down.tiled(), self.gate_weight)
 
 
 def pack_int4(q: torch.Tensor) -> torch.Tensor:

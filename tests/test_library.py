@@ -28,7 +28,7 @@ def test_library_loads_and_exports_every_symbol(pkg):
     lib = pkg._lib.load()
     for name in _declared_functions():
         assert hasattr(lib, name), name
-    assert lib.dflash_abi_version() == pkg._lib.ABI_VERSION == 1
+    assert lib.dflash_abi_version() == pkg._lib.ABI_VERSION == 2
 
 
 def test_library_has_no_unresolved_internal_symbols(pkg):
@@ -56,9 +56,9 @@ host_only = pytest.mark.skipif(
     reason="passes fake device pointers that must fail host validation; run only where no GPU is visible")
 
 
-def _desc(pkg, experts=1, rows=512, cols=2048, group=128, dtype=0, packed=16, scales=16):
+def _desc(pkg, experts=1, rows=512, cols=2048, group=128, dtype=0, packed=16, scales=16, layout=0):
     return pkg._lib.W4Desc(packed=packed, scales=scales, experts=experts, rows=rows, cols=cols, group_size=group,
-                           scale_dtype=dtype)
+                           scale_dtype=dtype, layout=layout)
 
 
 def _status(pkg, name, *args):
@@ -89,6 +89,37 @@ def test_qlinear_validation(pkg):
     assert st == 3 and "workspace" in msg
     st, _ = _status(pkg, "dflash_qlinear_w4a16", None, 0, ctypes.byref(d), None, None, 0, None)
     assert st == 0  # m == 0 is a no-op
+
+
+@host_only
+def test_to_tiled_validation(pkg):
+    out = ctypes.c_void_p(1 << 20)
+    st, msg = _status(pkg, "dflash_w4_to_tiled", None, out, out, None)
+    assert st == 1 and "NULL" in msg
+    d = _desc(pkg, rows=40)
+    st, msg = _status(pkg, "dflash_w4_to_tiled", ctypes.byref(d), out, out, None)
+    assert st == 2 and "rows % 16" in msg
+    d = _desc(pkg, layout=1)
+    st, msg = _status(pkg, "dflash_w4_to_tiled", ctypes.byref(d), out, out, None)
+    assert st == 1 and "PORTABLE" in msg
+    d = _desc(pkg, layout=5)
+    st, msg = _status(pkg, "dflash_w4_to_tiled", ctypes.byref(d), out, out, None)
+    assert st == 1 and "layout" in msg
+    d = _desc(pkg)
+    st, msg = _status(pkg, "dflash_w4_to_tiled", ctypes.byref(d), ctypes.c_void_p(16), out, None)
+    assert st == 1 and "alias" in msg
+    st, msg = _status(pkg, "dflash_w4_to_tiled", ctypes.byref(d), ctypes.c_void_p((1 << 20) + 8), out, None)
+    assert st == 1 and "aligned" in msg
+
+
+@host_only
+def test_tiled_weights_refused_where_no_kernel_reads_them(pkg):
+    """qlinear with group 256 and m > 32 has no tiled-reading kernel: status 2 before any launch."""
+    ws = ctypes.c_void_p(4096)
+    d = _desc(pkg, rows=64, cols=1024, group=256, layout=1)
+    st, msg = _status(pkg, "dflash_qlinear_w4a16", ctypes.c_void_p(16), 33, ctypes.byref(d), ctypes.c_void_p(16), ws,
+                      1 << 20, None)
+    assert st == 2 and "tiled" in msg
 
 
 @host_only

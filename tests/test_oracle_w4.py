@@ -94,3 +94,34 @@ def test_product_packer_matches_oracle(pkg, group, scale_dtype):
     q = np.clip(np.rint(w.numpy().reshape(3, 64, -1, group) / s.numpy()[..., None]), -8, 7).reshape(w.shape)
     np.testing.assert_array_equal(w4.unpack(packed.packed.numpy()), q.astype(np.int8))
     assert float(s[0, 0, 0]) == 1.0
+
+
+@pytest.mark.parametrize("lead,n,k,groups", [((), 16, 256, 2), ((2,), 32, 512, 4), ((3,), 48, 256, 1)])
+def test_to_tiled_follows_the_bytewise_definition(lead, n, k, groups):
+    """Chunk l of block (t, b) is bytes 64b + 16(l // 16) .. +15 of row 16t + l % 16; scales [t][g][c] = [16t + c][g]."""
+    rng = np.random.default_rng(n + k)
+    packed = rng.integers(0, 256, (*lead, n, k // 2), dtype=np.uint8)
+    scales = rng.random((*lead, n, groups)).astype(np.float32)
+    tiled, tiled_s = w4.to_tiled(packed, scales)
+    assert tiled.shape == packed.shape and tiled_s.shape == scales.shape
+    flat_p = packed.reshape(-1, n, k // 2)
+    flat_t = tiled.reshape(flat_p.shape[0], -1)
+    flat_s = scales.reshape(-1, n, groups)
+    flat_ts = tiled_s.reshape(flat_s.shape[0], -1)
+    for e in range(flat_p.shape[0]):
+        for t in range(n // 16):
+            for b in range(k // 128):
+                for lane in range(64):
+                    o = (t * (k // 128) + b) * 1024 + lane * 16
+                    src = flat_p[e, 16 * t + lane % 16, 64 * b + 16 * (lane // 16): 64 * b + 16 * (lane // 16) + 16]
+                    assert (flat_t[e, o:o + 16] == src).all()
+            for g in range(groups):
+                for c in range(16):
+                    assert flat_ts[e, (t * groups + g) * 16 + c] == flat_s[e, 16 * t + c, g]
+    back, back_s = w4.from_tiled(tiled, tiled_s)
+    assert (back == packed).all() and (back_s == scales).all()
+
+
+def test_to_tiled_rejects_untileable_shapes():
+    with pytest.raises(ValueError):
+        w4.to_tiled(np.zeros((24, 64), np.uint8), np.zeros((24, 1), np.float32))
