@@ -288,8 +288,8 @@ struct RouteOut {
 };
 
 int run_verify(const MoeShapes& S, dflash::VerifyParams gu, dflash::VerifyParams dn, const RouteOut& ro,
-               const int32_t* inv, void* ws, const MoeLayout& L, const dflash_w4* gate_up, const dflash_w4* down,
-               const dflash_w4* sgu, const dflash_w4* sdn, void* out, hipStream_t stream) {
+               const int32_t* inv, const float* wts, void* ws, const MoeLayout& L, const dflash_w4* gate_up,
+               const dflash_w4* down, const dflash_w4* sgu, const dflash_w4* sdn, void* out, hipStream_t stream) {
   using namespace dflash;
   const int T = static_cast<int>(S.T), H = static_cast<int>(S.H), I = static_cast<int>(S.I);
   W4StreamParams p{};
@@ -361,7 +361,9 @@ int run_verify(const MoeShapes& S, dflash::VerifyParams gu, dflash::VerifyParams
   if (int r = launch_status("down")) return r;
 
   if (measuring()) return DFLASH_OK;
-  launch_combine(at<float>(ws, L.y), inv, T, p.top_k, H, p.has_shared, static_cast<uint16_t*>(out), stream);
+  // the verify down launch leaves y unweighted: the combine applies the routing weights
+  launch_combine(at<float>(ws, L.y), inv, T, p.top_k, H, p.has_shared, wts, at<float>(ws, L.gate),
+                 static_cast<uint16_t*>(out), stream);
   return launch_status("combine");
 }
 
@@ -448,7 +450,7 @@ int run_experts(const MoeShapes& S, const int32_t* inv, void* ws, const MoeLayou
   if (int r = launch_status("down")) return r;
 
   if (measuring()) return DFLASH_OK;
-  launch_combine(at<float>(ws, L.y), inv, T, k, H, p.has_shared, static_cast<uint16_t*>(out), stream);
+  launch_combine(at<float>(ws, L.y), inv, T, k, H, p.has_shared, nullptr, nullptr, static_cast<uint16_t*>(out), stream);
   return launch_status("combine");
 }
 
@@ -698,8 +700,8 @@ int dflash_moe_experts_w4a16(const void* hidden, int64_t tokens, int64_t hidden_
     if (!measuring()) dflash::launch_table_prep(t, st);
     if (int r = launch_status("table_prep")) return r;
     if (verify)
-      return run_verify(S, vgu, vdn, RouteOut{}, inv_perm, workspace, L, gate_up, down, shared_gate_up, shared_down,
-                        out, st);
+      return run_verify(S, vgu, vdn, RouteOut{}, inv_perm, topk_weights, workspace, L, gate_up, down, shared_gate_up,
+                        shared_down, out, st);
     return run_experts(S, inv_perm, workspace, L, gate_up, down, shared_gate_up, shared_down, out, st);
   } catch (...) {
     return fail(DFLASH_ERR_HIP, "unexpected host exception");
@@ -766,7 +768,7 @@ int dflash_moe_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, co
     if (tokens == 0) return DFLASH_OK;
     if (verify)
       return run_verify(S, vgu, vdn, RouteOut{logits, topk_ids, topk_weights, perm, inv_perm, expert_offsets},
-                        inv_perm, workspace, L, gate_up, down, shared_gate_up, shared_down, out, st);
+                        inv_perm, topk_weights, workspace, L, gate_up, down, shared_gate_up, shared_down, out, st);
     return run_experts(S, inv_perm, workspace, L, gate_up, down, shared_gate_up, shared_down, out, st);
   } catch (...) {
     return fail(DFLASH_ERR_HIP, "unexpected host exception");

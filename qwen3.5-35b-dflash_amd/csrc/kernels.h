@@ -140,8 +140,10 @@ __host__ __device__ inline int route_slot_pitch(int T) { return (T + 15) & ~15; 
 int64_t route_zero_words(int T, int E);
 void launch_route(const RouteParams& p, bool zeroed, hipStream_t stream);
 void launch_table_prep(const TableParams& p, hipStream_t stream);
-void launch_combine(const float* y, const int32_t* inv, int T, int k, int H, int has_shared, uint16_t* out,
-                    hipStream_t stream);
+// out = bf16(sum over slots of y rows): rows pre-weighted when wts is null, else weighted
+// here by wts [T*k] (flat pair order) and gate [T] (shared expert).
+void launch_combine(const float* y, const int32_t* inv, int T, int k, int H, int has_shared, const float* wts,
+                    const float* gate, uint16_t* out, hipStream_t stream);
 // Per-wave fallback for any K % 512 == 0 (w4_gemm.hip); max_slots bounds the hit experts + shared.
 void launch_w4_gemm(int mode, bool fp32_scales, int max_slots, const W4StreamParams& p, hipStream_t stream);
 // K in {512, 1024, 2048} and group 128 (spill-free register budgets); K = 512 splits 4 ways with 2 row groups,
@@ -163,12 +165,13 @@ void launch_w4_wave(int mode, bool fp32_scales, int grid, const W4StreamParams& 
 struct VerifyParams {
   W4StreamParams g;
   // dynamic LDS layout, byte offsets (verify_layout)
-  int lds_a, lds_neg, lds_tok, lds_pdesc, lds_wgt, lds_part, lds_scratch, lds_bytes;
+  int lds_a, lds_neg, lds_tok, lds_pdesc, lds_wgt, lds_part, lds_scratch, lds_bytes;  // lds_wgt: down's raw partials
   int pd_cap;        // pass descriptors the LDS holds
   int a_rows;        // activation rows the LDS holds (gate/up: T; linear: M; down: chunk_passes * 16)
   int chunk_passes;  // down: passes whose h rows are staged at once
-  // in-kernel routing (gate/up only): fp32 logits [T][E] -> the dflash_moe_route outputs
-  // (written by workgroup 0) and the work table of the down launch
+  // in-kernel routing (gate/up only; 1: one wave per token, 2: one 16-lane row per token):
+  // fp32 logits [T][E] -> the dflash_moe_route outputs (written by workgroup 0) and the
+  // work table of the down launch
   int route, E;
   const float* logits;
   int32_t* ids;

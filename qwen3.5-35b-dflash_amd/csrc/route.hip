@@ -564,11 +564,15 @@ __global__ __launch_bounds__(512) void table_prep_kernel(TableParams p) {
 
 // ---------------------------------------------------------------------------
 // Combine: out[t] = sum_slot y[inv[t*k+slot]] (+ y[T*k + t] for the shared
-// expert), fp32 in slot order, one bf16 rounding.  grid = (T, H / 512),
+// expert), fp32 in slot order, one bf16 rounding.  When wts is given the rows
+// are unweighted expert outputs and each is scaled first: by wts[t*k+slot]
+// (the routing weight) or gate[t] (the shared-expert sigmoid) -- the same fp32
+// product the expert epilogues otherwise apply.  grid = (T, H / 512),
 // block = 64: a lane owns 8 columns; the rows are read 8 at a time, all loads
 // of a batch in flight together, and added in slot order.
 __global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ y, const int32_t* __restrict__ inv, int T,
-                                                     int k, int H, int has_shared, uint16_t* __restrict__ out) {
+                                                     int k, int H, int has_shared, const float* __restrict__ wts,
+                                                     const float* __restrict__ gate, uint16_t* __restrict__ out) {
   const int t = blockIdx.x;
   const int c = (blockIdx.y * 64 + threadIdx.x) * 8;
   const int nrows = k + (has_shared ? 1 : 0);
@@ -576,6 +580,7 @@ __global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ y
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int s0 = 0; s0 < nrows; s0 += 8) {
       float4 a[8], b[8];
+      float w[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int s = min(s0 + i, nrows - 1);
@@ -583,10 +588,15 @@ __global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ y
         const float4* src = reinterpret_cast<const float4*>(y + row * H + c);
         a[i] = src[0];
         b[i] = src[1];
+        w[i] = wts == nullptr ? 1.f : (s < k ? ld_const(wts, t * k + s) : ld_const(gate, t));
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         if (s0 + i < nrows) {
+          if (wts != nullptr) {
+            a[i].x *= w[i]; a[i].y *= w[i]; a[i].z *= w[i]; a[i].w *= w[i];
+            b[i].x *= w[i]; b[i].y *= w[i]; b[i].z *= w[i]; b[i].w *= w[i];
+          }
           acc[0] += a[i].x; acc[1] += a[i].y; acc[2] += a[i].z; acc[3] += a[i].w;
           acc[4] += b[i].x; acc[5] += b[i].y; acc[6] += b[i].z; acc[7] += b[i].w;
         }
@@ -645,10 +655,11 @@ void launch_table_prep(const TableParams& p, hipStream_t stream) {
   hipLaunchKernelGGL(table_prep_kernel, dim3(1 + p.T), dim3(512), 0, stream, p);
 }
 
-void launch_combine(const float* y, const int32_t* inv, int T, int k, int H, int has_shared, uint16_t* out,
-                    hipStream_t stream) {
+void launch_combine(const float* y, const int32_t* inv, int T, int k, int H, int has_shared, const float* wts,
+                    const float* gate, uint16_t* out, hipStream_t stream) {
   if (T <= 0) return;
-  hipLaunchKernelGGL(combine_kernel, dim3(T, (H + 511) / 512), dim3(64), 0, stream, y, inv, T, k, H, has_shared, out);
+  hipLaunchKernelGGL(combine_kernel, dim3(T, (H + 511) / 512), dim3(64), 0, stream, y, inv, T, k, H, has_shared, wts,
+                     gate, out);
 }
 
 }  // namespace dflash

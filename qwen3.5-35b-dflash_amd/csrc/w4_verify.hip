@@ -27,17 +27,19 @@
 //             its -136*sum terms and the token of every slot row in LDS; the
 //             epilogue writes h = silu(g)*u in bf16 and its -136*sum per 16
 //             columns.
-//   down    : stages the h rows of its passes (chunks that fit in LDS); the
-//             epilogue writes y = route_weight * (h . Wd^T) in fp32, which the
-//             combine kernel sums over slots.  (Combining inside this launch
-//             would need an agent-scope release per workgroup, an L2 write-back
-//             on every XCD, which measured slower than one more launch.)
+//   down    : stages the h rows of its passes and their -136*sum partials
+//             (chunks that fit in LDS), all by direct-to-LDS loads; the epilogue
+//             writes the unweighted y = h . Wd^T in fp32, which the combine
+//             kernel scales by the routing weights and sums over slots.
+//             (Combining inside this launch would need an agent-scope release
+//             per workgroup, an L2 write-back on every XCD, which measured
+//             slower than one more launch.)
 //   linear  : x rows of a plain qlinear (one pass per 16 rows).
 //
 // Semantics per mode (reference citations):
 //   kModeLinear : y = x . dequant(W)^T, bf16 out                 (fused/quantization.py:154-165)
 //   kModeGateUp : h = silu(x.Wg^T) * (x.Wu^T), gate rows first   (reference/fused_ops.py:170-171)
-//   kModeDown   : y = route_weight * (h . Wd^T), fp32            (fused/quantization.py:196-199)
+//   kModeDown   : y = h . Wd^T, fp32 (the combine weighs it)   (fused/quantization.py:196-199)
 //   routing     : top-k, renormalised softmax, stable permutation (reference/fused_ops.py:160-164,
 //                                                                   fused/quantization.py:184-191)
 #include <algorithm>
@@ -203,6 +205,202 @@ __device__ int route_block(const VerifyParams& vp, char* lds, int4* pdesc, int* 
   return routed + shared_passes;
 }
 
+// ---------------------------------------------------------------------------
+// Row-parallel routing of the block (E <= 256, k <= 16, T <= 32): one 16-lane
+// row per token, so the selection rounds are row-local DPP reductions with no
+// scalar round trips, and four tokens share every instruction.  Lane r of a
+// row holds the keys of experts kPR r .. kPR r + kPR - 1 (16-byte loads), so
+// expert ids grow with the lane and, inside a lane, with the key index.  Same
+// contract as route_block.
+template <int kPR>
+struct RowKeys {
+  uint32_t key[kPR];
+};
+
+// Max (kMin false) or min over the 16 lanes of a row, in every lane of the row.
+template <bool kMin>
+__device__ __forceinline__ uint32_t row_reduce(uint32_t v) {
+  auto f = [](uint32_t a, uint32_t b) { return kMin ? (a < b ? a : b) : (a > b ? a : b); };
+  v = f(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xB1, 0xF, 0xF, false)));   // quad_perm [1,0,3,2]
+  v = f(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x4E, 0xF, 0xF, false)));   // quad_perm [2,3,0,1]
+  v = f(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x141, 0xF, 0xF, false)));  // row_half_mirror
+  v = f(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x140, 0xF, 0xF, false)));  // row_mirror
+  return v;
+}
+
+__device__ __forceinline__ float row_sum_f32(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
+  return v;
+}
+
+// Inclusive prefix sum over the 64 lanes (row shifts, then row broadcasts).
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 into rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 into rows 2, 3
+  return v;
+}
+
+// The keys of this lane's row token (token 4 * wave + row); issued first so the
+// caller's staging loads queue behind them.
+template <int kPR>
+__device__ __forceinline__ RowKeys<kPR> route_rows_load(const VerifyParams& vp) {
+  const int T = vp.g.T, E = vp.E;
+  const int t = 4 * (threadIdx.x >> 6) + ((threadIdx.x >> 4) & 3), r = threadIdx.x & 15;
+  // rows past T repeat the last token (never recorded); the buffer resource reads 0 past E
+  const buf_rsrc lr = make_rsrc(vp.logits + static_cast<int64_t>(min(t, T - 1)) * E, static_cast<uint32_t>(E) * 4);
+  RowKeys<kPR> k;
+  float v[kPR];
+#pragma unroll
+  for (int i = 0; i < kPR; i += 4) {
+    const uint4 q = buf_load16(lr, static_cast<uint32_t>((kPR * r + i) * 4), 0);
+    v[i] = __uint_as_float(q.x);
+    if (i + 1 < kPR) v[i + 1] = __uint_as_float(q.y);
+    if (i + 2 < kPR) v[i + 2] = __uint_as_float(q.z);
+    if (i + 3 < kPR) v[i + 3] = __uint_as_float(q.w);
+  }
+#pragma unroll
+  for (int i = 0; i < kPR; ++i) {
+    const int e = kPR * r + i;
+    k.key[i] = e < E ? sortable_key(v[i]) + 1u : 0u;  // sortable keys stay below 0xFF800001
+  }
+  return k;
+}
+
+template <int kPR>
+__device__ int route_rows(const VerifyParams& vp, RowKeys<kPR> keys, char* lds, int4* pdesc, int* tok) {
+  const int T = vp.g.T, E = vp.E, k = vp.g.top_k;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id(), r = lane & 15;
+  const int t = 4 * wave + (lane >> 4);
+  const int tpad = (T + 3) & ~3;
+  const bool out = blockIdx.x == 0;
+  int* cnt = reinterpret_cast<int*>(lds + vp.lds_scratch);        // [256] tokens per expert, then its first slot row
+  float* rw = reinterpret_cast<float*>(cnt + 256);                // [T*k] routing weight of every flat pair
+  int* rid = reinterpret_cast<int*>(rw + 512);                    // [T*k] expert of every flat pair
+  int* wtot = rid + 512;                                          // [3][4] wave totals: slot rows, passes, hits
+  uint32_t* map_words = reinterpret_cast<uint32_t*>(wtot + 12);   // [E][tpad] bytes: slot + 1, or 0
+  uint8_t* map = reinterpret_cast<uint8_t*>(map_words);
+  for (int i = tid; i < 256; i += kVThreads) cnt[i] = 0;
+  for (int i = tid; i < (E * tpad) / 4; i += kVThreads) map_words[i] = 0u;
+
+  // ---- k selection rounds per row: largest key, lowest expert id among equal keys;
+  // lane s of the row keeps slot s
+  int my_id = 0;
+  uint32_t my_key = 0, top_key = 0;
+  if (4 * wave < T) {  // waves whose rows are all past T stay off the VALU
+    for (int s = 0; s < k; ++s) {
+      uint32_t lm = keys.key[0];
+#pragma unroll
+      for (int i = 1; i < kPR; ++i) lm = lm > keys.key[i] ? lm : keys.key[i];
+      const uint32_t rm = row_reduce<false>(lm);
+      uint32_t cand = 0xFFFFu;
+#pragma unroll
+      for (int i = kPR - 1; i >= 0; --i) cand = keys.key[i] == rm ? static_cast<uint32_t>(kPR * r + i) : cand;
+      const uint32_t e = row_reduce<true>(cand);
+      const uint32_t ie = static_cast<uint32_t>(kPR * r) <= e && e < static_cast<uint32_t>(kPR * r + kPR)
+                              ? e - static_cast<uint32_t>(kPR * r) : 0xFFFFu;
+#pragma unroll
+      for (int i = 0; i < kPR; ++i) keys.key[i] = ie == static_cast<uint32_t>(i) ? 0u : keys.key[i];
+      if (s == 0) top_key = rm - 1u;
+      if (r == s) {
+        my_id = static_cast<int>(e);
+        my_key = rm - 1u;
+      }
+    }
+  }
+  // renormalised softmax over the selected logits (the full-softmax denominator cancels)
+  const float ex = r < k ? expf(key_to_float(my_key) - key_to_float(top_key)) : 0.f;
+  const float w = ex / row_sum_f32(ex);
+  __syncthreads();  // the counters are cleared
+  if (t < T && r < k) {
+    rw[t * k + r] = w;
+    rid[t * k + r] = my_id;
+    atomicAdd(&cnt[my_id], 1);
+    map[my_id * tpad + t] = static_cast<uint8_t>(r + 1);
+    if (out) {
+      vp.ids[t * k + r] = my_id;
+      vp.wts[t * k + r] = w;
+    }
+  }
+  __syncthreads();
+
+  // ---- exclusive scans over experts (threads 0..255, one expert each): first slot row, first pass
+  const int c = tid < E ? cnt[tid] : 0;
+  const int np = passes_for(c, 16);
+  const int ia = wave_inclusive_scan(c), ic = wave_inclusive_scan(np);
+  const int wh = __builtin_popcountll(__ballot(c > 0));
+  if (tid < 256 && lane == 63) {
+    wtot[wave] = ia;
+    wtot[4 + wave] = ic;
+    wtot[8 + wave] = wh;
+  }
+  __syncthreads();
+  int ba = 0, bc = 0, hits = 0, routed = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (i < wave) {
+      ba += wtot[i];
+      bc += wtot[4 + i];
+    }
+    routed += wtot[4 + i];
+    hits += wtot[8 + i];
+  }
+  const int off = ba + ia - c, p0 = bc + ic - np;
+  if (tid < E) {
+    if (out) vp.offsets[tid] = off;
+    for (int i = 0; i < np; ++i) {
+      const int4 d = make_int4(tid, off, c, 16 * i);
+      pdesc[p0 + i] = d;
+      if (out) vp.pass_table_out[p0 + i] = d;
+    }
+  }
+  const int shared_passes = vp.g.has_shared ? passes_for(T, 16) : 0;
+  if (tid < shared_passes) {
+    const int4 d = make_int4(-1, 0, T, 16 * tid);
+    pdesc[routed + tid] = d;
+    if (out) vp.pass_table_out[routed + tid] = d;
+  }
+  if (out && tid == 0) {
+    vp.offsets[E] = T * k;
+    vp.meta_out[0] = hits;
+    vp.meta_out[1] = routed + shared_passes;
+  }
+  __syncthreads();  // every count is read: cnt becomes each expert's first slot row
+  if (tid < E) cnt[tid] = off;
+  __syncthreads();
+  // ---- stable permutation: pair (token tt, slot) goes to its expert's segment after the
+  // expert's tokens below tt (nonzero bytes of the slot-map row before column tt)
+  for (int i = tid; i < T * k; i += kVThreads) {
+    const int tt = i / k;
+    const int e = rid[i];
+    const uint32_t* row = map_words + (e * tpad) / 4;
+    int before = 0;
+    for (int q = 0; q * 4 < tt; ++q) {
+      uint32_t word = row[q];
+      const int lim = tt - q * 4;  // columns of this word below tt (>= 1)
+      if (lim < 4) word &= (1u << (8 * lim)) - 1u;
+      const uint32_t zero_hi = ~(((word & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | word | 0x7F7F7F7Fu);  // 0x80 per zero byte
+      before += 4 - __popc(zero_hi);
+    }
+    const int pos = cnt[e] + before;
+    tok[pos] = tt;
+    if (out) {
+      vp.perm[pos] = i;
+      vp.inv[i] = pos;
+      vp.slot_w_out[pos] = rw[i];
+      vp.tok_out[pos] = tt;
+    }
+  }
+  __syncthreads();
+  return routed + shared_passes;
+}
+
 }  // namespace
 
 template <int kMode, int kNKB, typename ScaleT>
@@ -221,12 +419,38 @@ __global__ __launch_bounds__(512) void w4_verify_kernel(VerifyParams vp) {
   float* lds_neg = reinterpret_cast<float*>(lds + vp.lds_neg);
   int* lds_tok = reinterpret_cast<int*>(lds + vp.lds_tok);
   int4* lds_pdesc = reinterpret_cast<int4*>(lds + vp.lds_pdesc);
-  float* lds_wgt = reinterpret_cast<float*>(lds + vp.lds_wgt);
+  float* lds_hpart = reinterpret_cast<float*>(lds + vp.lds_wgt);  // down: raw -136*sum partials of the h rows
   f32x4* lds_part = reinterpret_cast<f32x4*>(lds + vp.lds_part);  // [wave][2][64]
 
-  // ---- passes of the launch
+  // x rows (octet-interleaved) in 1 KB blocks and their -136*sum terms, by direct-to-LDS loads
+  auto stage_x = [&]() {
+    const int rows = kMode == kModeLinear ? p.M : p.T;
+    const buf_rsrc xr = make_rsrc(p.act, static_cast<uint32_t>(rows) * kK * 2);
+    constexpr int kBlk = kK / 512;  // 1 KB blocks per row
+    for (int i = wave; i < rows * kBlk; i += kVWaves) {
+      const int r = i / kBlk, bl = i - r * kBlk;
+      dma16(xr, lds_a + r * kRS + bl * 1024, static_cast<uint32_t>(lane * 16),
+            static_cast<uint32_t>((r * kK + bl * 512) * 2));
+    }
+    const buf_rsrc nr = make_rsrc(p.act_neg, static_cast<uint32_t>(rows) * kNKB * 4);
+    for (int i = wave; i * 64 < rows * kNKB; i += kVWaves)
+      dma4(nr, lds_neg + i * 64, static_cast<uint32_t>(lane * 4), static_cast<uint32_t>(i * 256));
+  };
+
+  // ---- passes of the launch; in-kernel routing stages x while it routes
   int total_passes;
-  if (kMode == kModeGateUp && vp.route) {
+  if (kMode == kModeGateUp && vp.route == 2) {
+    if (vp.E <= 64) {
+      const RowKeys<4> keys = route_rows_load<4>(vp);
+      stage_x();
+      total_passes = route_rows<4>(vp, keys, lds, lds_pdesc, lds_tok);
+    } else {
+      const RowKeys<16> keys = route_rows_load<16>(vp);
+      stage_x();
+      total_passes = route_rows<16>(vp, keys, lds, lds_pdesc, lds_tok);
+    }
+  } else if (kMode == kModeGateUp && vp.route) {
+    stage_x();
     total_passes = route_block(vp, lds, lds_pdesc, lds_tok);
   } else if (kMode == kModeLinear) {
     total_passes = (p.M + 15) >> 4;
@@ -262,61 +486,7 @@ __global__ __launch_bounds__(512) void w4_verify_kernel(VerifyParams vp) {
     const int Pc_end = min(P_last + 1, Pc + chunk_passes);
     const int cb = max(ub, Pc * strips), ce = min(ue, Pc_end * strips);
     if (Pc != P_first) __syncthreads();  // every wave is done with the previous chunk's rows
-
-    // ---- stage the chunk's activation rows and descriptors
-    if (kMode == kModeGateUp || kMode == kModeLinear) {
-      if (!(kMode == kModeGateUp && vp.route)) {
-        pd_base = Pc;
-        if (kMode == kModeGateUp)
-          for (int i = tid; i < Pc_end - Pc; i += kVThreads) lds_pdesc[i] = p.pass_table[Pc + i];
-      }
-      // x rows: 1 KB blocks by direct-to-LDS loads; the -136*sum terms; the token of every slot row
-      const int rows = kMode == kModeLinear ? p.M : p.T;
-      const buf_rsrc xr = make_rsrc(p.act, static_cast<uint32_t>(rows) * kK * 2);
-      constexpr int kBlk = kK / 512;  // 1 KB blocks per row
-      for (int i = wave; i < rows * kBlk; i += kVWaves) {
-        const int r = i / kBlk, bl = i - r * kBlk;
-        dma16(xr, lds_a + r * kRS + bl * 1024, static_cast<uint32_t>(lane * 16), static_cast<uint32_t>((r * kK + bl * 512) * 2));
-      }
-      const buf_rsrc nr = make_rsrc(p.act_neg, static_cast<uint32_t>(rows) * kNKB * 4);
-      for (int i = wave; i * 64 < rows * kNKB; i += kVWaves)
-        dma4(nr, lds_neg + i * 64, static_cast<uint32_t>(lane * 4), static_cast<uint32_t>(i * 256));
-      if (kMode == kModeGateUp && !vp.route)
-        for (int i = tid; i < p.T * p.top_k; i += kVThreads) lds_tok[i] = p.tok[i];
-    } else {
-      // down: per pass of the chunk its 16 h rows (clamped to the slot), -136*sum terms
-      // (8 partials of 16 columns per k-block) and routing weights
-      pd_base = Pc;
-      const int npass = Pc_end - Pc;
-      for (int i = tid; i < npass; i += kVThreads) lds_pdesc[i] = p.pass_table[Pc + i];
-      const int hrows = p.T * p.top_k + (p.has_shared ? p.T : 0);
-      const buf_rsrc hr = make_rsrc(p.act, static_cast<uint32_t>(hrows) * kK * 2);
-      constexpr int kBlk = kK / 512;
-      for (int i = wave; i < npass * 16 * kBlk; i += kVWaves) {
-        const int rr = i / kBlk, bl = i - rr * kBlk;
-        const int4 d = ld_const_int4(p.pass_table, Pc + rr / 16);
-        const int base = d.x < 0 ? p.T * p.top_k : d.y;
-        const int row = base + min(d.w + (rr & 15), d.z - 1);
-        dma16(hr, lds_a + rr * kRS + bl * 1024, static_cast<uint32_t>(lane * 16),
-              static_cast<uint32_t>((row * kK + bl * 512) * 2));
-      }
-      for (int i = tid; i < npass * 16 * kNKB; i += kVThreads) {
-        const int rr = i / kNKB, kb = i - rr * kNKB;
-        const int4 d = p.pass_table[Pc + rr / 16];
-        const int base = d.x < 0 ? p.T * p.top_k : d.y;
-        const int row = base + min(d.w + (rr & 15), d.z - 1);
-        const float4* ns = reinterpret_cast<const float4*>(p.act_neg + (static_cast<int64_t>(row) * kNKB + kb) * 8);
-        const float4 u = ns[0], v = ns[1];
-        lds_neg[i] = ((u.x + u.y) + (u.z + u.w)) + ((v.x + v.y) + (v.z + v.w));
-      }
-      for (int i = tid; i < npass * 16; i += kVThreads) {
-        const int4 d = p.pass_table[Pc + i / 16];
-        const int m = min(d.w + (i & 15), d.z - 1);
-        lds_wgt[i] = d.x < 0 ? p.shared_gate[m] : p.slot_w[d.y + m];
-      }
-    }
-    wait_vmem();
-    __syncthreads();
+    bool staged = false;  // the chunk's rows and descriptors are in LDS
 
     // ---- this wave's k-blocks of the chunk: [g0, g1), an exact eighth of them
     const int n = (ce - cb) * kNKB;
@@ -348,12 +518,11 @@ __global__ __launch_bounds__(512) void w4_verify_kernel(VerifyParams vp) {
           const float part = row16_sum(valid ? bf16_to_f32(hb) : 0.f);
           if (valid && lr == 0) p.out_part[static_cast<int64_t>(hrow) * (inter >> 4) + strip] = -kDequantOffset * part;
         } else {
-          if (valid) {
-            const float wg = lds_wgt[(P - Pc) * 16 + 4 * kq + e];
+          if (valid) {  // unweighted: the combine applies the routing weight
             const int yrow = shared ? p.T * p.top_k + m : cd.y + m;
             float* o = p.out_f32 + static_cast<int64_t>(yrow) * p.N + row0 + lr;
-            o[0] = t0[e] * wg;
-            o[16] = t1[e] * wg;
+            o[0] = t0[e];
+            o[16] = t1[e];
           }
         }
       }
@@ -361,7 +530,7 @@ __global__ __launch_bounds__(512) void w4_verify_kernel(VerifyParams vp) {
 
     f32x4 head0 = zero, head1 = zero;
     int head_unit = -1;  // chunk-relative unit this wave ends but did not begin
-    if (g0 < g1) {
+    {
       // load cursor: next k-block to issue and the bases of its unit
       int lg = g0, l_ur = -1;
       const uint8_t* l_w = nullptr;
@@ -369,7 +538,10 @@ __global__ __launch_bounds__(512) void w4_verify_kernel(VerifyParams vp) {
       auto unit_bases = [&](int ur) {
         const int u = cb + ur;
         const int P = u / strips, strip = u - P * strips;
-        const int4 d = pass_desc(P);
+        // before the staging barrier the descriptor comes from the work table (s_load),
+        // except after in-kernel routing, whose table is only in LDS
+        const int4 d = staged || (kMode == kModeGateUp && vp.route) || kMode == kModeLinear
+                           ? pass_desc(P) : ld_const_int4(p.pass_table, P);
         const bool shared = kMode != kModeLinear && d.x < 0;
         const int64_t e = kMode == kModeLinear ? 0 : d.x;
         const uint8_t* wbase = shared ? p.w_shared : p.w + e * p.w_stride;
@@ -385,7 +557,7 @@ __global__ __launch_bounds__(512) void w4_verify_kernel(VerifyParams vp) {
       // Loads are issued unconditionally (past the range they repeat its last k-block, never
       // computed): a load under a branch would make the compiler drain the queue at the loop edge.
       auto issue = [&](uint4 (&dst)[2], uint32_t (&sdst)[2]) {
-        const int lc = min(lg, g1 - 1);
+        const int lc = max(min(lg, g1 - 1), 0);
         const int ur = lc / kNKB, kb = lc - ur * kNKB;
         if (ur != l_ur) {
           l_ur = ur;
@@ -398,8 +570,65 @@ __global__ __launch_bounds__(512) void w4_verify_kernel(VerifyParams vp) {
         sdst[1] = load_scale_bits(sp + second * kNKB);
         ++lg;
       };
+      // the first k-blocks go out before the activations are staged (they do not depend on them)
 #pragma unroll
       for (int i = 0; i + 1 < kVDepth; ++i) issue(wbuf[i], sbuf[i]);
+
+      // ---- stage the chunk's activation rows and descriptors
+      if (kMode == kModeGateUp || kMode == kModeLinear) {
+        if (!(kMode == kModeGateUp && vp.route)) {
+          // the token of every slot row and the chunk's pass descriptors (in-kernel routing
+          // left both in LDS and staged x already)
+          pd_base = Pc;
+          if (kMode == kModeGateUp) {
+            for (int i = tid; i < Pc_end - Pc; i += kVThreads) lds_pdesc[i] = p.pass_table[Pc + i];
+            for (int i = tid; i < p.T * p.top_k; i += kVThreads) lds_tok[i] = p.tok[i];
+          }
+          stage_x();
+        }
+      } else {
+        // down: the chunk's pass descriptors, per pass its 16 h rows (clamped to the slot) and
+        // their -136*sum partials (8 per k-block, one per 16 columns), all by direct-to-LDS
+        // loads so the prologue's weight loads are not waited for ahead of them
+        pd_base = Pc;
+        const int npass = Pc_end - Pc;
+        const buf_rsrc tr = make_rsrc(p.pass_table, static_cast<uint32_t>(total_passes) * 16);
+        if (wave == 0)
+          dma16(tr, lds_pdesc, static_cast<uint32_t>(min(Pc + lane, total_passes - 1) * 16), 0);
+        const int hrows = p.T * p.top_k + (p.has_shared ? p.T : 0);
+        const buf_rsrc hr = make_rsrc(p.act, static_cast<uint32_t>(hrows) * kK * 2);
+        constexpr int kBlk = kK / 512;
+        for (int i = wave; i < npass * 16 * kBlk; i += kVWaves) {
+          const int rr = i / kBlk, bl = i - rr * kBlk;
+          const int4 d = ld_const_int4(p.pass_table, Pc + rr / 16);
+          const int base = d.x < 0 ? p.T * p.top_k : d.y;
+          const int row = base + min(d.w + (rr & 15), d.z - 1);
+          dma16(hr, lds_a + rr * kRS + bl * 1024, static_cast<uint32_t>(lane * 16),
+                static_cast<uint32_t>((row * kK + bl * 512) * 2));
+        }
+        constexpr int kPartRow = kNKB * 8;  // partials per h row
+        const buf_rsrc pr = make_rsrc(p.act_neg, static_cast<uint32_t>(hrows) * kPartRow * 4);
+        for (int i = wave; i < npass * 2 * kNKB; i += kVWaves) {  // 64 partials per load, 2 kNKB per pass
+          const int pass = i / (2 * kNKB), j = i - pass * 2 * kNKB;
+          const int4 d = ld_const_int4(p.pass_table, Pc + pass);
+          const int base = d.x < 0 ? p.T * p.top_k : d.y;
+          const int f = 64 * j + lane, rr = f / kPartRow;
+          const int row = base + min(d.w + rr, d.z - 1);
+          dma4(pr, lds_hpart + pass * 16 * kPartRow + 64 * j, static_cast<uint32_t>((row * kPartRow + f % kPartRow) * 4), 0);
+        }
+      }
+      wait_vmem();
+      __syncthreads();
+      if (kMode == kModeDown) {
+        // -136*sum(h) per 128 columns from its 8 partials (same order as the partial writer's readers)
+        for (int i = tid; i < (Pc_end - Pc) * 16 * kNKB; i += kVThreads) {
+          const float4 u = *reinterpret_cast<const float4*>(lds_hpart + 8 * i);
+          const float4 v = *reinterpret_cast<const float4*>(lds_hpart + 8 * i + 4);
+          lds_neg[i] = ((u.x + u.y) + (u.z + u.w)) + ((v.x + v.y) + (v.z + v.w));
+        }
+        __syncthreads();
+      }
+      staged = true;
 
       // compute state of the current unit
       int c_ur = -1, P = 0, a_off = 0;
@@ -519,17 +748,18 @@ bool verify_layout(int mode, int T, int K, int N, int E, int k, int has_shared, 
   VerifyParams& L = *vp;
   L.route = 0;
   if (mode == kModeDown) {
-    const int per_pass = 16 * rs + al(16 * nkb * 4) + al(16 * 4) + 16;
-    const int fixed = part;
+    // per pass: 16 h rows, their -136*sum terms and raw partials (8 per k-block)
+    const int per_pass = 16 * rs + al(16 * nkb * 4) + al(16 * nkb * 8 * 4);
+    const int fixed = part + 64 * 16;  // partial sums of split units; 64 pass descriptors (one load)
     const int cp = std::min(8, (kVLds - fixed) / per_pass);
     if (cp < 1) return false;
     L.chunk_passes = cp;
-    L.pd_cap = cp;
+    L.pd_cap = 64;
     L.a_rows = cp * 16;
     L.lds_a = take(cp * 16 * rs);
     L.lds_neg = take(cp * 16 * nkb * 4);
-    L.lds_wgt = take(cp * 16 * 4);
-    L.lds_pdesc = take(cp * 16);
+    L.lds_wgt = take(cp * 16 * nkb * 8 * 4);
+    L.lds_pdesc = take(64 * 16);
     L.lds_tok = 0;
     L.lds_part = L.lds_scratch = take(part);
     L.lds_bytes = off;
@@ -552,8 +782,13 @@ bool verify_layout(int mode, int T, int K, int N, int E, int k, int has_shared, 
   L.lds_tok = take(T * k * 4);
   L.lds_pdesc = take(L.pd_cap * 16);
   const int base = off;
-  const int scratch = al(((E + 3) & ~3) * 4) + al(((T * k + 3) & ~3) * 4) + 96 + E * ((T + 3) & ~3);
-  if (route && E <= 2 * kVThreads && base + std::max(part, al(scratch)) <= kVLds) {
+  const int tpad = (T + 3) & ~3;
+  const int scratch = al(((E + 3) & ~3) * 4) + al(((T * k + 3) & ~3) * 4) + 96 + E * tpad;
+  const int row_scratch = (256 + 512 + 512 + 12) * 4 + E * tpad;  // route_rows: counts, weights, ids, totals, map
+  if (route && E <= 256 && k <= 16 && T * k <= 512 && base + std::max(part, row_scratch) <= kVLds) {
+    L.route = 2;
+    L.lds_part = L.lds_scratch = take(std::max(part, row_scratch));
+  } else if (route && E <= 2 * kVThreads && base + std::max(part, al(scratch)) <= kVLds) {
     L.route = 1;
     L.lds_part = L.lds_scratch = take(std::max(part, scratch));
   } else {
