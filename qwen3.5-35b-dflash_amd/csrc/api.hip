@@ -450,7 +450,11 @@ int run_experts(const MoeShapes& S, const int32_t* inv, void* ws, const MoeLayou
   if (int r = launch_status("down")) return r;
 
   if (measuring()) return DFLASH_OK;
-  launch_combine(at<float>(ws, L.y), inv, T, k, H, p.has_shared, nullptr, nullptr, static_cast<uint16_t*>(out), stream);
+  if (path == GemmPath::kTile)
+    launch_combine_bf16(at<uint16_t>(ws, L.y), inv, T, k, H, p.has_shared, static_cast<uint16_t*>(out), stream);
+  else
+    launch_combine(at<float>(ws, L.y), inv, T, k, H, p.has_shared, nullptr, nullptr, static_cast<uint16_t*>(out),
+                   stream);
   return launch_status("combine");
 }
 

@@ -119,7 +119,7 @@ struct W4StreamParams {
   // outputs
   uint16_t* out_bf16;      // kModeLinear: [M][N]; kModeGateUp: h [(T*k+T)][N/2] interleaved
   float* out_part;         // kModeGateUp: [(T*k+T)][N/32] partial -136*sum(h) per 16 columns ([N/256] per 128 on the tile kernel)
-  float* out_f32;          // kModeDown: y [(T*k+T)][N]
+  float* out_f32;          // kModeDown: y [(T*k+T)][N] (the tile kernel writes it as bf16)
   const float* slot_w;     // kModeDown: routing weight of every slot row [T*k]
   const float* shared_gate;// kModeDown: sigmoid gate [T]
   int M;                   // kModeLinear rows
@@ -144,6 +144,9 @@ void launch_table_prep(const TableParams& p, hipStream_t stream);
 // here by wts [T*k] (flat pair order) and gate [T] (shared expert).
 void launch_combine(const float* y, const int32_t* inv, int T, int k, int H, int has_shared, const float* wts,
                     const float* gate, uint16_t* out, hipStream_t stream);
+// The same over weighted bf16 y rows (the prefill tile path).
+void launch_combine_bf16(const uint16_t* y, const int32_t* inv, int T, int k, int H, int has_shared, uint16_t* out,
+                         hipStream_t stream);
 // Per-wave fallback for any K % 512 == 0 (w4_gemm.hip); max_slots bounds the hit experts + shared.
 void launch_w4_gemm(int mode, bool fp32_scales, int max_slots, const W4StreamParams& p, hipStream_t stream);
 // K in {512, 1024, 2048} and group 128 (spill-free register budgets); K = 512 splits 4 ways with 2 row groups,
@@ -190,7 +193,9 @@ bool verify_layout(int mode, int T, int K, int N, int E, int k, int has_shared, 
 void launch_w4_verify(int mode, bool fp32_scales, int grid, const VerifyParams& vp, hipStream_t stream);
 // LDS-tiled kernel for long prefill (w4_tile.hip): 96-row passes, column tiles of 512
 // (p.strips = I / 256 for gate_up, H / 512 for down), K % 512 == 0; its gate_up writes one
-// -136*sum(h) per 128 columns and its down reads them that way.
+// -136*sum(h) per 128 columns and its down reads them that way; its down writes weighted
+// y rows in bf16 (launch_combine_bf16).  Workgroups take tiles from a queue in meta[2]
+// (gate/up) / meta[3] (down), zero on entry and left zero.
 constexpr int kTileRowsPerPass = 96;
 bool w4_tile_supports(int mode, int N, int K, int G);
 void launch_w4_tile(int mode, bool fp32_scales, int grid, const W4StreamParams& p, hipStream_t stream);

@@ -345,6 +345,8 @@ __global__ __launch_bounds__(1024) void route_small_kernel(RouteParams p) {
       p.pass_start[nh + p.has_shared] = total;
       p.meta[0] = nh;
       p.meta[1] = total;
+      p.meta[2] = 0;  // tile-queue counters of the prefill expert kernels
+      p.meta[3] = 0;
     }
   }
   // stable ranks: expert tid walks its slot-map row (tokens ascending)
@@ -470,6 +472,8 @@ __global__ __launch_bounds__(256) void route_permute_kernel(RouteParams p) {
       p.pass_start[nh + p.has_shared] = total;
       p.meta[0] = nh;
       p.meta[1] = total;
+      p.meta[2] = 0;  // tile-queue counters of the prefill expert kernels
+      p.meta[3] = 0;
     }
   }
   if (cnt == 0) return;
@@ -559,18 +563,22 @@ __global__ __launch_bounds__(512) void table_prep_kernel(TableParams p) {
     p.pass_start[h + p.has_shared] = total;
     p.meta[0] = h;
     p.meta[1] = total;
+    p.meta[2] = 0;  // tile-queue counters of the prefill expert kernels
+    p.meta[3] = 0;
   }
 }
 
 // ---------------------------------------------------------------------------
 // Combine: out[t] = sum_slot y[inv[t*k+slot]] (+ y[T*k + t] for the shared
-// expert), fp32 in slot order, one bf16 rounding.  When wts is given the rows
+// expert), fp32 in slot order, one bf16 rounding.  y rows are fp32, or bf16
+// (the prefill tile path, already weighted).  When wts is given the rows
 // are unweighted expert outputs and each is scaled first: by wts[t*k+slot]
 // (the routing weight) or gate[t] (the shared-expert sigmoid) -- the same fp32
 // product the expert epilogues otherwise apply.  grid = (T, H / 512),
 // block = 64: a lane owns 8 columns; the rows are read 8 at a time, all loads
 // of a batch in flight together, and added in slot order.
-__global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ y, const int32_t* __restrict__ inv, int T,
+template <typename YT>
+__global__ __launch_bounds__(64) void combine_kernel(const YT* __restrict__ y, const int32_t* __restrict__ inv, int T,
                                                      int k, int H, int has_shared, const float* __restrict__ wts,
                                                      const float* __restrict__ gate, uint16_t* __restrict__ out) {
   const int t = blockIdx.x;
@@ -585,9 +593,17 @@ __global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ y
       for (int i = 0; i < 8; ++i) {
         const int s = min(s0 + i, nrows - 1);
         const int64_t row = s < k ? ld_const(inv, t * k + s) : static_cast<int64_t>(T) * k + t;
-        const float4* src = reinterpret_cast<const float4*>(y + row * H + c);
-        a[i] = src[0];
-        b[i] = src[1];
+        if constexpr (sizeof(YT) == 4) {
+          const float4* src = reinterpret_cast<const float4*>(y + row * H + c);
+          a[i] = src[0];
+          b[i] = src[1];
+        } else {  // bf16 rows: 8 columns in one 16-byte load
+          const uint4 v = *reinterpret_cast<const uint4*>(y + row * H + c);
+          a[i] = make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xFFFF0000u),
+                             __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xFFFF0000u));
+          b[i] = make_float4(__uint_as_float(v.z << 16), __uint_as_float(v.z & 0xFFFF0000u),
+                             __uint_as_float(v.w << 16), __uint_as_float(v.w & 0xFFFF0000u));
+        }
         w[i] = wts == nullptr ? 1.f : (s < k ? ld_const(wts, t * k + s) : ld_const(gate, t));
       }
 #pragma unroll
@@ -658,8 +674,15 @@ void launch_table_prep(const TableParams& p, hipStream_t stream) {
 void launch_combine(const float* y, const int32_t* inv, int T, int k, int H, int has_shared, const float* wts,
                     const float* gate, uint16_t* out, hipStream_t stream) {
   if (T <= 0) return;
-  hipLaunchKernelGGL(combine_kernel, dim3(T, (H + 511) / 512), dim3(64), 0, stream, y, inv, T, k, H, has_shared, wts,
-                     gate, out);
+  hipLaunchKernelGGL(combine_kernel<float>, dim3(T, (H + 511) / 512), dim3(64), 0, stream, y, inv, T, k, H, has_shared,
+                     wts, gate, out);
+}
+
+void launch_combine_bf16(const uint16_t* y, const int32_t* inv, int T, int k, int H, int has_shared, uint16_t* out,
+                         hipStream_t stream) {
+  if (T <= 0) return;
+  hipLaunchKernelGGL(combine_kernel<uint16_t>, dim3(T, (H + 511) / 512), dim3(64), 0, stream, y, inv, T, k, H,
+                     has_shared, nullptr, nullptr, out);
 }
 
 }  // namespace dflash

@@ -277,9 +277,11 @@ __device__ __forceinline__ void tile_pass(const W4StreamParams& p, const TileLds
         const int m = d.w + r;
         const int yrow = c.shared ? p.T * p.top_k + m : d.y + m;
         const float wgt = c.shared ? p.shared_gate[m] : p.slot_w[d.y + m];
-        float* o = p.out_f32 + static_cast<int64_t>(yrow) * p.N + c.nt * kTileN + wave * 64 + lr;
+        // weighted, in bf16: halves the y traffic of this launch and the combine's
+        uint16_t* o = reinterpret_cast<uint16_t*>(p.out_f32) + static_cast<int64_t>(yrow) * p.N + c.nt * kTileN +
+                      wave * 64 + lr;
 #pragma unroll
-        for (int f = 0; f < 4; ++f) o[f * 16] = u[ms][f][e] * s_prev[f] * wgt;
+        for (int f = 0; f < 4; ++f) o[f * 16] = f32_to_bf16(u[ms][f][e] * s_prev[f] * wgt);
       }
     }
   }
@@ -361,11 +363,30 @@ __global__ __launch_bounds__(512) void w4_tile_kernel(W4StreamParams p) {
   __shared__ uint4 w0[kWaves * 4 * 64], w1[kWaves * 4 * 64], w2[kWaves * 4 * 64];
   __shared__ uint32_t s0[kWaves * 64], s1[kWaves * 64], s2[kWaves * 64];
   const TileLds lds{{a0, a1}, {n0, n1}, {w0, w1, w2}, {s0, s1, s2}};
+  __shared__ int next_tile;
   const int ntiles = p.strips;  // column tiles per pass
-  const int total = ld_const(p.meta, 1) * ntiles;
-  for (int tile = blockIdx.x; tile < total; tile += gridDim.x) {
-    const int P = tile / ntiles;
-    run_tile<kMode, ScaleT>(p, lds, P, tile - P * ntiles);
+  const int passes = ld_const(p.meta, 1);
+  const int total = passes * ntiles;
+  // heaviest tiles first: the shared expert's full passes (the last passes of the table),
+  // then the routed experts' in table order
+  const int sp = p.has_shared ? (p.T + kTileM - 1) / kTileM : 0;
+  // Each workgroup takes its first tile by index, then asks a queue for more; every
+  // workgroup that ran a tile makes exactly one failing request, so the queue ends at
+  // `total` and the request that returns total - 1 is the launch's last: it resets the
+  // queue for the next launch.  Nothing waits on the queue.
+  int* queue = const_cast<int*>(p.meta) + (kMode == kModeGateUp ? 2 : 3);
+  for (int tile = blockIdx.x; tile < total;) {
+    const int i = tile / ntiles;
+    const int P = i < sp ? passes - sp + i : i - sp;
+    run_tile<kMode, ScaleT>(p, lds, P, tile - i * ntiles);
+    if (threadIdx.x == 0) {
+      const int got = __hip_atomic_fetch_add(queue, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (got == total - 1) __hip_atomic_store(queue, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      next_tile = static_cast<int>(gridDim.x) + got;
+    }
+    __syncthreads();
+    tile = next_tile;
+    __syncthreads();  // every wave has read next_tile before thread 0 may write it again
   }
 }
 
