@@ -12,12 +12,17 @@ multi-layer verify forward would be issued), so host launch overhead is not
 part of the measurement.
 
 Prints ONE JSON line.  ``value`` is microseconds per MoE layer (lower is
-better).  ``roofline`` is the dominant kernel, the grouped gate/up GEMM:
-HIP events on its launch stream bracket graph replays that hold only that
-kernel's launches (measurement mode of the library), one per step over the
-same rotation of weight sets and hidden blocks; achieved = its algorithmic
-bytes (int4 gate/up rows + bf16 scales of the hit experts and the shared
-expert, x in, h out) / mean launch duration.
+better).  ``roofline`` is the dominant kernel, the grouped gate/up launch as it
+runs in the layer (it routes the block in its prologue, from the step's router
+logits, then streams the hit experts' gate/up rows): HIP events on its launch
+stream bracket graph replays that hold only that kernel's launches
+(measurement mode of the library), one per step over the same rotation of
+weight sets and hidden blocks; achieved = its algorithmic bytes (int4 gate/up
+rows + bf16 scales of the hit experts and the shared expert, x in, h out) /
+mean launch duration.  ``traffic`` is the HBM bytes the same kernel moves per
+launch, from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes recorded in
+``profiles/hbm_traffic_gate_up_t16.json`` (scaled by the counters' reading of a
+plain copy of known size), or null when that file is absent.
 ``prefill`` reports the T=2048 layer in TFLOP/s against bf16 MFMA peak.
 ``cpu_baseline`` times the oracle's CPU restatement of the same layer.
 """
@@ -157,7 +162,7 @@ def time_experts(pkg, sets, blocks, top_k, steps, warmup, workspace):
 GATE_UP_BYTES_PER_EXPERT = 2 * 512 * 2048 // 2 + 2 * 512 * (2048 // 128) * 2   # int4 + bf16 scales
 
 
-def time_stage(pkg, sets, blocks, top_k, steps, warmup, stage=None):
+def time_stage(pkg, sets, blocks, top_k, steps, warmup, stage=None, given_logits=False):
     """Average launch duration of one expert-stage kernel, timed with HIP events.
 
     For each of `period` steps (weight set j % sets, hidden block j % blocks)
@@ -173,24 +178,38 @@ def time_stage(pkg, sets, blocks, top_k, steps, warmup, stage=None):
     device = blocks[0].device
     nbytes = pkg.ops.moe_workspace_bytes(blocks[0].shape[0], 2048, 512, 256, top_k, 128, True)
     wss = [torch.empty(nbytes, dtype=torch.uint8, device=device) for _ in range(period)]
+    # with given_logits the calls pass each step's router logits, so the verify gate/up kernel
+    # routes in its prologue exactly as inside the layer; else it reads the work table
+    logits = [pkg.ops.router_logits(blocks[j % len(blocks)], sets[j % len(sets)][3]) for j in range(period)]
     hits = []
-    for j in range(period):
+
+    def call(j):
         gu, dn, sh, router = sets[j % len(sets)]
-        _, r, _ = pkg.ops.moe_w4a16(blocks[j % len(blocks)], gu, dn, top_k=top_k, router_weight=router, shared=sh,
-                                    workspace=wss[j], return_routing=True)
+        kw = {"router_logits": logits[j % period]} if given_logits else {"router_weight": router}
+        return pkg.ops.moe_w4a16(blocks[j % len(blocks)], gu, dn, top_k=top_k, shared=sh, workspace=wss[j % period],
+                                 return_routing=True, **kw)
+    for j in range(period):
+        _, r, _ = call(j)
         hits.append(int((r.offsets[1:] > r.offsets[:-1]).sum().item()))
     torch.cuda.synchronize()
 
     def step(j):
-        gu, dn, sh, router = sets[j % len(sets)]
-        pkg.ops.moe_w4a16(blocks[j % len(blocks)], gu, dn, top_k=top_k, router_weight=router, shared=sh,
-                          workspace=wss[j % period])
+        call(j)
     pkg.ops.set_measure_stage(stage)
     try:
         ms = time_steps(step, steps, warmup, period)
     finally:
         pkg.ops.set_measure_stage(0)
     return ms, statistics.mean(hits)
+
+
+def measured_traffic():
+    """HBM bytes per gate/up launch from the committed counter passes, or None."""
+    path = ROOT / "profiles" / "hbm_traffic_gate_up_t16.json"
+    if not path.is_file():
+        return None
+    rec = json.loads(path.read_text())
+    return int(round((rec["fetch_kib"] * rec["fetch_scale"] + rec["write_kib"] * rec["write_scale"]) * 1024))
 
 
 def cpu_baseline(pkg, tokens, top_k, seconds_budget=20.0):
@@ -239,6 +258,8 @@ def main() -> int:
     ap.add_argument("--sets", type=int, default=3, help="independent weight sets rotated per step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a plain 256 MiB device copy (reference dispatch for HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (the MoE layer would shard by "
@@ -257,6 +278,14 @@ def main() -> int:
     ws = torch.empty(pkg.ops.moe_workspace_bytes(2048, 2048, 512, 256, top_k, 128, True), dtype=torch.uint8,
                      device=device)
 
+    if args.calibrate_copy:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=device).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     log("timing the T=16 layer")
     ms = time_layer(pkg, sets, blocks, top_k, args.steps, args.warmup, ws)
     log("timing the expert stage")
@@ -265,7 +294,8 @@ def main() -> int:
     all_bytes = (hits + 1) * (INT4_BYTES_PER_EXPERT + SCALE_BYTES_PER_EXPERT)
     layer_gbs = int4_bytes / (ms * 1e-3) / 1e9
     log("timing the gate/up kernel with HIP events")
-    gu_ms, gu_hits = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup)
+    gu_ms, gu_hits = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup, given_logits=True)
+    stream_ms, _ = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup)
     dn_ms, _ = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup, pkg.ops.STAGE_DOWN)
     # algorithmic bytes of one gate/up launch: the hit experts' and the shared
     # expert's int4 gate/up rows + bf16 scales, x read, h (bf16) written
@@ -285,12 +315,13 @@ def main() -> int:
         "layer_int4_gbs": round(layer_gbs, 1),
         "layer_hbm_frac_int4": round(layer_gbs / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "w4_verify_kernel<1, 16, unsigned short> (grouped gate/up + SiLU*up, T=16, "
-                               "tiled banks)",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "kernel": "w4_verify_kernel<1, 16, unsigned short> (routing prologue + grouped gate/up "
+                               "+ SiLU*up, T=16, tiled banks)",
                      "kernel_us": round(gu_ms * 1e3, 2), "hit_experts_mean": round(gu_hits, 2),
                      "bytes_per_launch": int(gu_bytes)},
         "stages": {"expert_stage_us": round(exp_ms * 1e3, 2), "down_kernel_us": round(dn_ms * 1e3, 2),
+                   "gate_up_stream_only_us": round(stream_ms * 1e3, 2),
                    "expert_int4_bytes": int(int4_bytes), "expert_weight_bytes": int(all_bytes),
                    "expert_stage_int4_gbs": round(int4_bytes / (exp_ms * 1e-3) / 1e9, 1)},
     }

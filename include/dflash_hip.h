@@ -162,8 +162,10 @@ int dflash_moe_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, co
  * as usual but launch only that stage's kernel, which reads the routing, work
  * table and intermediate activations that an earlier full call with the same
  * arguments left in the same workspace, and writes the same intermediate
- * output again (out is not written).  DFLASH_STAGE_NONE restores full calls.
- * Process-wide.
+ * output again (out is not written).  On the verify path (T <= 32) the gate/up
+ * kernel also routes the block in its prologue; in measurement mode it does so
+ * only when the call passes router_logits (else it reads the work table).
+ * DFLASH_STAGE_NONE restores full calls.  Process-wide.
  */
 enum dflash_stage {
   DFLASH_STAGE_NONE = 0,

@@ -279,6 +279,7 @@ bool verify_fits(const MoeShapes& S, bool route, dflash::VerifyParams* gu, dflas
 
 // Routing outputs the gate/up launch writes when it routes in its prologue.
 struct RouteOut {
+  bool logits_given;  // the caller's logits (valid in measurement mode too)
   const float* logits;
   int32_t* ids;
   float* wts;
@@ -320,8 +321,9 @@ int run_verify(const MoeShapes& S, dflash::VerifyParams gu, dflash::VerifyParams
   p.strips = I / 16;
   gu.g = p;
   gu.E = static_cast<int>(S.E);
-  // measurement mode times the GEMM on the work table an earlier full call left
-  if (measuring()) gu.route = 0;
+  // measurement mode routes again only from the caller's logits (valid without the front
+  // launch); otherwise it times the GEMM on the work table an earlier full call left
+  if (measuring() && !ro.logits_given) gu.route = 0;
   if (gu.route) {
     gu.logits = ro.logits;
     gu.ids = ro.ids;
@@ -771,7 +773,8 @@ int dflash_moe_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, co
     }
     if (tokens == 0) return DFLASH_OK;
     if (verify)
-      return run_verify(S, vgu, vdn, RouteOut{logits, topk_ids, topk_weights, perm, inv_perm, expert_offsets},
+      return run_verify(S, vgu, vdn,
+                        RouteOut{router_logits != nullptr, logits, topk_ids, topk_weights, perm, inv_perm, expert_offsets},
                         inv_perm, topk_weights, workspace, L, gate_up, down, shared_gate_up, shared_down, out, st);
     return run_experts(S, inv_perm, workspace, L, gate_up, down, shared_gate_up, shared_down, out, st);
   } catch (...) {

@@ -34,6 +34,18 @@ __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 // need no conservative full wait on every iteration.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS operations
+// (lgkmcnt(0)) but not for its vector-memory loads still in flight.
+// __syncthreads() also waits for vmcnt(0), i.e. for a prefetch pipeline's worth
+// of outstanding global loads, every time.  The empty asm statements keep the
+// compiler from moving memory accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left at their maxima
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Load of a wave-uniform element through the constant address space: with a
 // readfirstlane'd index it becomes s_load (counted by lgkmcnt), so it never
 // waits behind the vector loads a wave keeps in flight.  Only for memory the

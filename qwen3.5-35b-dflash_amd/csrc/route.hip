@@ -216,7 +216,7 @@ __device__ __forceinline__ void router_big_tile(const uint16_t* __restrict__ x, 
         sa[st][slot0] = ra[i];
         sb[st][slot0] = rb0[i];
         sb[st][slot1] = rb1[i];
-        __syncthreads();
+        lds_barrier();  // the later chunks' loads stay in flight
         const int c = min(ch + kAhead, nch - 1) * 16;
         ra[i] = ga[c];
         rb0[i] = gb0[c];

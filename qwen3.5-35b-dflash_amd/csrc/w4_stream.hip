@@ -305,7 +305,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(W4StreamParams p) {
       }
       compute_unit<kMT, kKBPW, ScaleT>(cur, A, cd.M - m0, red.v[buf][wave]);
     }
-    __syncthreads();
+    lds_barrier();  // partial sums are in LDS; the prefetched units' loads stay in flight
     if (live) {
       const int colblock = c_strip * RG + rg;
       const int row0 = colblock * kTileRows;

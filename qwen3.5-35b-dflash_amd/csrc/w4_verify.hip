@@ -208,7 +208,8 @@ __device__ int route_block(const VerifyParams& vp, char* lds, int4* pdesc, int* 
 // ---------------------------------------------------------------------------
 // Row-parallel routing of the block (E <= 256, k <= 16, T <= 32): one 16-lane
 // row per token, so the selection rounds are row-local DPP reductions with no
-// scalar round trips, and four tokens share every instruction.  Lane r of a
+// scalar round trips, and four tokens share every instruction.  Its barriers
+// order LDS only: the activation staging issued before it stays in flight.  Lane r of a
 // row holds the keys of experts kPR r .. kPR r + kPR - 1 (16-byte loads), so
 // expert ids grow with the lane and, inside a lane, with the key index.  Same
 // contract as route_block.
@@ -317,7 +318,7 @@ __device__ int route_rows(const VerifyParams& vp, RowKeys<kPR> keys, char* lds, 
   // renormalised softmax over the selected logits (the full-softmax denominator cancels)
   const float ex = r < k ? expf(key_to_float(my_key) - key_to_float(top_key)) : 0.f;
   const float w = ex / row_sum_f32(ex);
-  __syncthreads();  // the counters are cleared
+  lds_barrier();  // the counters are cleared
   if (t < T && r < k) {
     rw[t * k + r] = w;
     rid[t * k + r] = my_id;
@@ -328,7 +329,7 @@ __device__ int route_rows(const VerifyParams& vp, RowKeys<kPR> keys, char* lds, 
       vp.wts[t * k + r] = w;
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- exclusive scans over experts (threads 0..255, one expert each): first slot row, first pass
   const int c = tid < E ? cnt[tid] : 0;
@@ -340,7 +341,7 @@ __device__ int route_rows(const VerifyParams& vp, RowKeys<kPR> keys, char* lds, 
     wtot[4 + wave] = ic;
     wtot[8 + wave] = wh;
   }
-  __syncthreads();
+  lds_barrier();
   int ba = 0, bc = 0, hits = 0, routed = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -371,9 +372,9 @@ __device__ int route_rows(const VerifyParams& vp, RowKeys<kPR> keys, char* lds, 
     vp.meta_out[0] = hits;
     vp.meta_out[1] = routed + shared_passes;
   }
-  __syncthreads();  // every count is read: cnt becomes each expert's first slot row
+  lds_barrier();  // every count is read: cnt becomes each expert's first slot row
   if (tid < E) cnt[tid] = off;
-  __syncthreads();
+  lds_barrier();
   // ---- stable permutation: pair (token tt, slot) goes to its expert's segment after the
   // expert's tokens below tt (nonzero bytes of the slot-map row before column tt)
   for (int i = tid; i < T * k; i += kVThreads) {
@@ -397,7 +398,7 @@ __device__ int route_rows(const VerifyParams& vp, RowKeys<kPR> keys, char* lds, 
       vp.tok_out[pos] = tt;
     }
   }
-  __syncthreads();
+  lds_barrier();
   return routed + shared_passes;
 }
 
