@@ -170,7 +170,7 @@ int dflash_moe_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, co
 enum dflash_stage {
   DFLASH_STAGE_NONE = 0,
   DFLASH_STAGE_GATE_UP = 1, /* grouped gate/up GEMM + SiLU*up of the expert FFN */
-  DFLASH_STAGE_DOWN = 2     /* grouped down GEMM + routing weight of the expert FFN */
+  DFLASH_STAGE_DOWN = 2     /* grouped down GEMM of the expert FFN */
 };
 int dflash_set_measure_stage(int stage);
 

@@ -206,16 +206,17 @@ __device__ int route_block(const VerifyParams& vp, char* lds, int4* pdesc, int* 
 }
 
 // ---------------------------------------------------------------------------
-// Row-parallel routing of the block (E <= 256, k <= 16, T <= 32): one 16-lane
-// row per token, so the selection rounds are row-local DPP reductions with no
-// scalar round trips, and four tokens share every instruction.  Its barriers
-// order LDS only: the activation staging issued before it stays in flight.  Lane r of a
-// row holds the keys of experts kPR r .. kPR r + kPR - 1 (16-byte loads), so
+// Half-wave-parallel routing of the block (E <= 256, k <= 16, T <= 32): one
+// 32-lane half-wave per token (two tokens per wave, 16 per token pass), so the
+// selection rounds are DPP reductions inside the half-wave with no LDS or scalar
+// round trips, and all eight waves work on a 16-token block.  Its barriers order
+// LDS only: the activation staging issued before it stays in flight.  Lane r of a
+// half-wave holds the keys of experts kPR r .. kPR r + kPR - 1 (16-byte loads), so
 // expert ids grow with the lane and, inside a lane, with the key index.  Same
 // contract as route_block.
 template <int kPR>
 struct RowKeys {
-  uint32_t key[kPR];
+  uint32_t key[2][kPR];  // token passes 0 and 1 (tokens 16..31)
 };
 
 // Max (kMin false) or min over the 16 lanes of a row, in every lane of the row.
@@ -227,6 +228,43 @@ __device__ __forceinline__ uint32_t row_reduce(uint32_t v) {
   v = f(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x141, 0xF, 0xF, false)));  // row_half_mirror
   v = f(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x140, 0xF, 0xF, false)));  // row_mirror
   return v;
+}
+
+// Max (kMin false) or min over the 32 lanes of a half-wave, in every lane of it:
+// the row result, rows 1 and 3 folding in lane 15 of rows 0 and 2 (row_bcast:15;
+// rows 0 and 2 keep their own), then lanes 31 and 63 broadcast.
+template <bool kMin>
+__device__ __forceinline__ uint32_t half_reduce(uint32_t v) {
+  v = row_reduce<kMin>(v);
+  const uint32_t o = static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), 0x142, 0xA, 0xF, false));
+  v = kMin ? (v < o ? v : o) : (v > o ? v : o);
+  const uint32_t lo = __builtin_amdgcn_readlane(v, 31), hi = __builtin_amdgcn_readlane(v, 63);
+  return (threadIdx.x & 32) ? hi : lo;
+}
+
+// Largest of a lane's keys, and the lowest index holding a given key (kPR if none).
+template <int kPR>
+__device__ __forceinline__ uint32_t keys_max(const uint32_t (&k)[kPR]) {
+  uint32_t m[kPR];
+#pragma unroll
+  for (int i = 0; i < kPR; ++i) m[i] = k[i];
+#pragma unroll
+  for (int w = 1; w < kPR; w *= 2)
+#pragma unroll
+    for (int i = 0; i + w < kPR; i += 2 * w) m[i] = m[i] > m[i + w] ? m[i] : m[i + w];
+  return m[0];
+}
+template <int kPR>
+__device__ __forceinline__ uint32_t keys_first(const uint32_t (&k)[kPR], uint32_t v) {
+  uint32_t m[kPR];
+#pragma unroll
+  for (int i = 0; i < kPR; ++i) m[i] = k[i] == v ? static_cast<uint32_t>(i) : static_cast<uint32_t>(kPR);
+#pragma unroll
+  for (int w = 1; w < kPR; w *= 2)
+#pragma unroll
+    for (int i = 0; i + w < kPR; i += 2 * w) m[i] = m[i] < m[i + w] ? m[i] : m[i + w];
+  return m[0];
 }
 
 __device__ __forceinline__ float row_sum_f32(float v) {
@@ -248,28 +286,35 @@ __device__ __forceinline__ int wave_inclusive_scan(int v) {
   return v;
 }
 
-// The keys of this lane's row token (token 4 * wave + row); issued first so the
-// caller's staging loads queue behind them.
+// The keys of this lane's tokens (2 * wave + half-wave + 16 * pass); issued first
+// so the caller's staging loads queue behind them.
 template <int kPR>
 __device__ __forceinline__ RowKeys<kPR> route_rows_load(const VerifyParams& vp) {
   const int T = vp.g.T, E = vp.E;
-  const int t = 4 * (threadIdx.x >> 6) + ((threadIdx.x >> 4) & 3), r = threadIdx.x & 15;
-  // rows past T repeat the last token (never recorded); the buffer resource reads 0 past E
-  const buf_rsrc lr = make_rsrc(vp.logits + static_cast<int64_t>(min(t, T - 1)) * E, static_cast<uint32_t>(E) * 4);
+  const int r = threadIdx.x & 31;
   RowKeys<kPR> k;
-  float v[kPR];
 #pragma unroll
-  for (int i = 0; i < kPR; i += 4) {
-    const uint4 q = buf_load16(lr, static_cast<uint32_t>((kPR * r + i) * 4), 0);
-    v[i] = __uint_as_float(q.x);
-    if (i + 1 < kPR) v[i + 1] = __uint_as_float(q.y);
-    if (i + 2 < kPR) v[i + 2] = __uint_as_float(q.z);
-    if (i + 3 < kPR) v[i + 3] = __uint_as_float(q.w);
-  }
+  for (int tp = 0; tp < 2; ++tp) {
+    const int t = 2 * (threadIdx.x >> 6) + ((threadIdx.x >> 5) & 1) + 16 * tp;
+    float v[kPR];
+    if (tp == 0 || T > 16) {
+      // tokens past T repeat the last one (never recorded); the buffer resource reads 0 past E
+      const buf_rsrc lr = make_rsrc(vp.logits + static_cast<int64_t>(min(t, T - 1)) * E, static_cast<uint32_t>(E) * 4);
 #pragma unroll
-  for (int i = 0; i < kPR; ++i) {
-    const int e = kPR * r + i;
-    k.key[i] = e < E ? sortable_key(v[i]) + 1u : 0u;  // sortable keys stay below 0xFF800001
+      for (int i = 0; i < kPR; i += 4) {
+        const uint4 q = buf_load16(lr, static_cast<uint32_t>((kPR * r + i) * 4), 0);
+        v[i] = __uint_as_float(q.x);
+        v[i + 1] = __uint_as_float(q.y);
+        v[i + 2] = __uint_as_float(q.z);
+        v[i + 3] = __uint_as_float(q.w);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kPR; ++i) {
+      const int e = kPR * r + i;
+      // sortable keys stay below 0xFF800001; 0 marks no expert (or a taken one)
+      k.key[tp][i] = (tp == 0 || T > 16) && e < E ? sortable_key(v[i]) + 1u : 0u;
+    }
   }
   return k;
 }
@@ -277,8 +322,8 @@ __device__ __forceinline__ RowKeys<kPR> route_rows_load(const VerifyParams& vp) 
 template <int kPR>
 __device__ int route_rows(const VerifyParams& vp, RowKeys<kPR> keys, char* lds, int4* pdesc, int* tok) {
   const int T = vp.g.T, E = vp.E, k = vp.g.top_k;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id(), r = lane & 15;
-  const int t = 4 * wave + (lane >> 4);
+  const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id(), r = lane & 31;
+  const int t0 = 2 * wave + (lane >> 5);  // token of pass 0; pass 1 adds 16
   const int tpad = (T + 3) & ~3;
   const bool out = blockIdx.x == 0;
   int* cnt = reinterpret_cast<int*>(lds + vp.lds_scratch);        // [256] tokens per expert, then its first slot row
@@ -290,43 +335,52 @@ __device__ int route_rows(const VerifyParams& vp, RowKeys<kPR> keys, char* lds, 
   for (int i = tid; i < 256; i += kVThreads) cnt[i] = 0;
   for (int i = tid; i < (E * tpad) / 4; i += kVThreads) map_words[i] = 0u;
 
-  // ---- k selection rounds per row: largest key, lowest expert id among equal keys;
-  // lane s of the row keeps slot s
-  int my_id = 0;
-  uint32_t my_key = 0, top_key = 0;
-  if (4 * wave < T) {  // waves whose rows are all past T stay off the VALU
+  // ---- k selection rounds per half-wave: largest key, lowest expert id among equal keys;
+  // lane s of the half-wave keeps slot s.  Both token passes share the rounds.
+  const int npass = T > 16 ? 2 : 1;
+  int my_id[2] = {0, 0};
+  uint32_t my_key[2] = {0, 0}, top_key[2] = {0, 0};
+  if (2 * wave < T) {  // waves whose tokens are all past T stay off the VALU
     for (int s = 0; s < k; ++s) {
-      uint32_t lm = keys.key[0];
 #pragma unroll
-      for (int i = 1; i < kPR; ++i) lm = lm > keys.key[i] ? lm : keys.key[i];
-      const uint32_t rm = row_reduce<false>(lm);
-      uint32_t cand = 0xFFFFu;
+      for (int tp = 0; tp < 2; ++tp) {
+        if (tp < npass) {
+          const uint32_t rm = half_reduce<false>(keys_max<kPR>(keys.key[tp]));
+          const uint32_t first = keys_first<kPR>(keys.key[tp], rm);
+          const uint32_t e = half_reduce<true>(first < kPR ? static_cast<uint32_t>(kPR * r) + first : 0xFFFFu);
+          const uint32_t ie = e - static_cast<uint32_t>(kPR * r);  // wraps past kPR unless this lane's
 #pragma unroll
-      for (int i = kPR - 1; i >= 0; --i) cand = keys.key[i] == rm ? static_cast<uint32_t>(kPR * r + i) : cand;
-      const uint32_t e = row_reduce<true>(cand);
-      const uint32_t ie = static_cast<uint32_t>(kPR * r) <= e && e < static_cast<uint32_t>(kPR * r + kPR)
-                              ? e - static_cast<uint32_t>(kPR * r) : 0xFFFFu;
-#pragma unroll
-      for (int i = 0; i < kPR; ++i) keys.key[i] = ie == static_cast<uint32_t>(i) ? 0u : keys.key[i];
-      if (s == 0) top_key = rm - 1u;
-      if (r == s) {
-        my_id = static_cast<int>(e);
-        my_key = rm - 1u;
+          for (int i = 0; i < kPR; ++i) keys.key[tp][i] = ie == static_cast<uint32_t>(i) ? 0u : keys.key[tp][i];
+          if (s == 0) top_key[tp] = rm - 1u;
+          if (r == s) {
+            my_id[tp] = static_cast<int>(e);
+            my_key[tp] = rm - 1u;
+          }
+        }
       }
     }
   }
-  // renormalised softmax over the selected logits (the full-softmax denominator cancels)
-  const float ex = r < k ? expf(key_to_float(my_key) - key_to_float(top_key)) : 0.f;
-  const float w = ex / row_sum_f32(ex);
+  // renormalised softmax over the selected logits (the full-softmax denominator cancels);
+  // the k <= 16 slots sit in the first row of the half-wave
+  float w[2];
+#pragma unroll
+  for (int tp = 0; tp < 2; ++tp) {
+    const float ex = r < k ? expf(key_to_float(my_key[tp]) - key_to_float(top_key[tp])) : 0.f;
+    w[tp] = ex / row_sum_f32(ex);
+  }
   lds_barrier();  // the counters are cleared
-  if (t < T && r < k) {
-    rw[t * k + r] = w;
-    rid[t * k + r] = my_id;
-    atomicAdd(&cnt[my_id], 1);
-    map[my_id * tpad + t] = static_cast<uint8_t>(r + 1);
-    if (out) {
-      vp.ids[t * k + r] = my_id;
-      vp.wts[t * k + r] = w;
+#pragma unroll
+  for (int tp = 0; tp < 2; ++tp) {
+    const int t = t0 + 16 * tp;
+    if (t < T && r < k) {
+      rw[t * k + r] = w[tp];
+      rid[t * k + r] = my_id[tp];
+      atomicAdd(&cnt[my_id[tp]], 1);
+      map[my_id[tp] * tpad + t] = static_cast<uint8_t>(r + 1);
+      if (out) {
+        vp.ids[t * k + r] = my_id[tp];
+        vp.wts[t * k + r] = w[tp];
+      }
     }
   }
   lds_barrier();
@@ -404,9 +458,56 @@ __device__ int route_rows(const VerifyParams& vp, RowKeys<kPR> keys, char* lds, 
 
 }  // namespace
 
+// x rows (octet-interleaved) in 1 KB blocks and their -136*sum terms, by direct-to-LDS loads
+template <int kMode, int kNKB>
+__device__ __forceinline__ void stage_x(const VerifyParams& vp, char* lds) {
+  const W4StreamParams& p = vp.g;
+  constexpr int kK = kNKB * 128;
+  constexpr int kRS = kK * 2 + 16;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = lane_id();
+  uint8_t* lds_a = reinterpret_cast<uint8_t*>(lds + vp.lds_a);
+  float* lds_neg = reinterpret_cast<float*>(lds + vp.lds_neg);
+  const int rows = kMode == kModeLinear ? p.M : p.T;
+  const buf_rsrc xr = make_rsrc(p.act, static_cast<uint32_t>(rows) * kK * 2);
+  constexpr int kBlk = kK / 512;  // 1 KB blocks per row
+  for (int i = wave; i < rows * kBlk; i += kVWaves) {
+    const int r = i / kBlk, bl = i - r * kBlk;
+    dma16(xr, lds_a + r * kRS + bl * 1024, static_cast<uint32_t>(lane * 16),
+          static_cast<uint32_t>((r * kK + bl * 512) * 2));
+  }
+  const buf_rsrc nr = make_rsrc(p.act_neg, static_cast<uint32_t>(rows) * kNKB * 4);
+  for (int i = wave; i * 64 < rows * kNKB; i += kVWaves)
+    dma4(nr, lds_neg + i * 64, static_cast<uint32_t>(lane * 4), static_cast<uint32_t>(i * 256));
+}
+
+// Passes of the launch.  The gate/up launch routes the block here when asked
+// (its x staging is issued first and stays in flight meanwhile).
+template <int kMode, int kNKB>
+__device__ __forceinline__ int verify_passes(const VerifyParams& vp, char* lds) {
+  int* lds_tok = reinterpret_cast<int*>(lds + vp.lds_tok);
+  int4* lds_pdesc = reinterpret_cast<int4*>(lds + vp.lds_pdesc);
+  if (kMode == kModeGateUp && vp.route == 2) {
+    if (vp.E <= 128) {
+      const RowKeys<4> keys = route_rows_load<4>(vp);
+      stage_x<kMode, kNKB>(vp, lds);
+      return route_rows<4>(vp, keys, lds, lds_pdesc, lds_tok);
+    }
+    const RowKeys<8> keys = route_rows_load<8>(vp);
+    stage_x<kMode, kNKB>(vp, lds);
+    return route_rows<8>(vp, keys, lds, lds_pdesc, lds_tok);
+  }
+  if (kMode == kModeGateUp && vp.route) {
+    stage_x<kMode, kNKB>(vp, lds);
+    return route_block(vp, lds, lds_pdesc, lds_tok);
+  }
+  if (kMode == kModeLinear) return (vp.g.M + 15) >> 4;
+  return ld_const(vp.g.meta, 1);
+}
+
+// The streaming GEMM of one verify launch over `total_passes` passes.
 template <int kMode, int kNKB, typename ScaleT>
-__global__ __launch_bounds__(512) void w4_verify_kernel(VerifyParams vp) {
-  __shared__ __attribute__((aligned(16))) char lds[kVLds];
+__device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, const int total_passes) {
   const W4StreamParams& p = vp.g;
   constexpr int kK = kNKB * 128;
   constexpr int kRS = kK * 2 + 16;                  // LDS row stride (bytes) of an activation row
@@ -423,41 +524,6 @@ __global__ __launch_bounds__(512) void w4_verify_kernel(VerifyParams vp) {
   float* lds_hpart = reinterpret_cast<float*>(lds + vp.lds_wgt);  // down: raw -136*sum partials of the h rows
   f32x4* lds_part = reinterpret_cast<f32x4*>(lds + vp.lds_part);  // [wave][2][64]
 
-  // x rows (octet-interleaved) in 1 KB blocks and their -136*sum terms, by direct-to-LDS loads
-  auto stage_x = [&]() {
-    const int rows = kMode == kModeLinear ? p.M : p.T;
-    const buf_rsrc xr = make_rsrc(p.act, static_cast<uint32_t>(rows) * kK * 2);
-    constexpr int kBlk = kK / 512;  // 1 KB blocks per row
-    for (int i = wave; i < rows * kBlk; i += kVWaves) {
-      const int r = i / kBlk, bl = i - r * kBlk;
-      dma16(xr, lds_a + r * kRS + bl * 1024, static_cast<uint32_t>(lane * 16),
-            static_cast<uint32_t>((r * kK + bl * 512) * 2));
-    }
-    const buf_rsrc nr = make_rsrc(p.act_neg, static_cast<uint32_t>(rows) * kNKB * 4);
-    for (int i = wave; i * 64 < rows * kNKB; i += kVWaves)
-      dma4(nr, lds_neg + i * 64, static_cast<uint32_t>(lane * 4), static_cast<uint32_t>(i * 256));
-  };
-
-  // ---- passes of the launch; in-kernel routing stages x while it routes
-  int total_passes;
-  if (kMode == kModeGateUp && vp.route == 2) {
-    if (vp.E <= 64) {
-      const RowKeys<4> keys = route_rows_load<4>(vp);
-      stage_x();
-      total_passes = route_rows<4>(vp, keys, lds, lds_pdesc, lds_tok);
-    } else {
-      const RowKeys<16> keys = route_rows_load<16>(vp);
-      stage_x();
-      total_passes = route_rows<16>(vp, keys, lds, lds_pdesc, lds_tok);
-    }
-  } else if (kMode == kModeGateUp && vp.route) {
-    stage_x();
-    total_passes = route_block(vp, lds, lds_pdesc, lds_tok);
-  } else if (kMode == kModeLinear) {
-    total_passes = (p.M + 15) >> 4;
-  } else {
-    total_passes = ld_const(p.meta, 1);
-  }
   const int strips = p.strips;
   const int64_t total_units = static_cast<int64_t>(total_passes) * strips;
   const int ub = static_cast<int>(total_units * blockIdx.x / gridDim.x);
@@ -486,7 +552,7 @@ __global__ __launch_bounds__(512) void w4_verify_kernel(VerifyParams vp) {
   for (int Pc = P_first; Pc <= P_last; Pc += chunk_passes) {
     const int Pc_end = min(P_last + 1, Pc + chunk_passes);
     const int cb = max(ub, Pc * strips), ce = min(ue, Pc_end * strips);
-    if (Pc != P_first) __syncthreads();  // every wave is done with the previous chunk's rows
+    if (Pc != P_first) lds_barrier();  // every wave is done with the previous chunk's rows
     bool staged = false;  // the chunk's rows and descriptors are in LDS
 
     // ---- this wave's k-blocks of the chunk: [g0, g1), an exact eighth of them
@@ -585,7 +651,7 @@ __global__ __launch_bounds__(512) void w4_verify_kernel(VerifyParams vp) {
             for (int i = tid; i < Pc_end - Pc; i += kVThreads) lds_pdesc[i] = p.pass_table[Pc + i];
             for (int i = tid; i < p.T * p.top_k; i += kVThreads) lds_tok[i] = p.tok[i];
           }
-          stage_x();
+          stage_x<kMode, kNKB>(vp, lds);
         }
       } else {
         // down: the chunk's pass descriptors, per pass its 16 h rows (clamped to the slot) and
@@ -615,7 +681,8 @@ __global__ __launch_bounds__(512) void w4_verify_kernel(VerifyParams vp) {
           const int base = d.x < 0 ? p.T * p.top_k : d.y;
           const int f = 64 * j + lane, rr = f / kPartRow;
           const int row = base + min(d.w + rr, d.z - 1);
-          dma4(pr, lds_hpart + pass * 16 * kPartRow + 64 * j, static_cast<uint32_t>((row * kPartRow + f % kPartRow) * 4), 0);
+          dma4(pr, lds_hpart + pass * 16 * kPartRow + 64 * j,
+               static_cast<uint32_t>((row * kPartRow + f % kPartRow) * 4), 0);
         }
       }
       wait_vmem();
@@ -711,7 +778,7 @@ __global__ __launch_bounds__(512) void w4_verify_kernel(VerifyParams vp) {
         }
       }
     }
-    __syncthreads();  // partial sums of split units are in LDS
+    lds_barrier();  // partial sums of split units are in LDS
     if (head_unit >= 0) {
       // sum the partials of the waves before this one that share the unit, in wave order
       const int gs = head_unit * kNKB;
@@ -729,6 +796,13 @@ __global__ __launch_bounds__(512) void w4_verify_kernel(VerifyParams vp) {
       finish(head_unit, pass_desc((cb + head_unit) / strips), t0, t1);
     }
   }
+}
+
+template <int kMode, int kNKB, typename ScaleT>
+__global__ __launch_bounds__(512) void w4_verify_kernel(VerifyParams vp) {
+  __shared__ __attribute__((aligned(16))) char lds[kVLds];
+  const int total_passes = verify_passes<kMode, kNKB>(vp, lds);
+  verify_gemm<kMode, kNKB, ScaleT>(vp, lds, total_passes);
 }
 
 // ---------------------------------------------------------------------------
@@ -798,6 +872,7 @@ bool verify_layout(int mode, int T, int K, int N, int E, int k, int has_shared, 
   L.lds_bytes = off;
   return off <= kVLds;
 }
+
 
 void launch_w4_verify(int mode, bool fp32_scales, int grid, const VerifyParams& vp, hipStream_t stream) {
   const dim3 g(static_cast<unsigned>(grid)), blk(kVThreads);
