@@ -175,17 +175,28 @@ __device__ __forceinline__ void router_tile(const uint16_t* __restrict__ x, cons
   }
 }
 
+constexpr int kRouterAhead = 4;  // 128-column chunks of the big router tile in flight
+
 // Router logits for a 32-token x 64-expert tile (long T): the 128-column chunks
 // of both operands are staged once in LDS in MFMA fragment order (8 KB + 16 KB
-// per stage, two stages), fed from registers that keep kAhead chunks in
+// per stage, two stages), fed from registers that keep kRouterAhead chunks in
 // flight, and each of the 8 waves computes one 16 x 16 block over the whole of
-// H (H % 128 == 0).
+// H = 128 kNch.  The chunk loop is straight-line code: a loop around the ring
+// makes the compiler wait for every load in flight at its head.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // a plain vector: rings stay in registers
+struct RouterLds {
+  u32x4 sa[2][2 * 4 * 64];  // [stage][token subtile x k-step][lane]
+  u32x4 sb[2][4 * 4 * 64];  // [stage][expert subtile x k-step][lane]
+};
+
+template <int kNch>
 __device__ __forceinline__ void router_big_tile(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-                                                float* __restrict__ logits, int T, int E, int H, int t0, int e0) {
-  constexpr int kAhead = 8;
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // a plain vector: the ring stays in registers
-  __shared__ u32x4 sa[2][2 * 4 * 64];  // [stage][token subtile x k-step][lane]
-  __shared__ u32x4 sb[2][4 * 4 * 64];  // [stage][expert subtile x k-step][lane]
+                                                float* __restrict__ logits, int T, int E, int t0, int e0,
+                                                RouterLds& L) {
+  constexpr int kAhead = kRouterAhead < kNch ? kRouterAhead : kNch;
+  constexpr int H = kNch * 128;
+  auto& sa = L.sa;
+  auto& sb = L.sb;
   const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id();
   const int lr = lane & 15, kq = lane >> 4, tq = wave & 1, eq = wave >> 1;
   // staging: thread copies 16-byte chunk sc of token row sr and of expert rows sr and 32 + sr
@@ -196,45 +207,39 @@ __device__ __forceinline__ void router_big_tile(const uint16_t* __restrict__ x, 
   // fragment slot of (row r, chunk c): block (r / 16) * 4 + c / 4, lane r % 16 + 16 * (c % 4)
   const int frag = (sc >> 2) * 64 + (sr & 15) + 16 * (sc & 3);
   const int slot0 = (sr >> 4) * 4 * 64 + frag, slot1 = ((sr + 32) >> 4) * 4 * 64 + frag;
-  const int nch = H >> 7;
-  // the ring is indexed through static_for so its slots are constants before unrolling (registers)
+  // the ring is indexed through static_for so its slots are constants (registers)
   u32x4 ra[kAhead], rb0[kAhead], rb1[kAhead];
   static_for(std::make_integer_sequence<int, kAhead>{}, [&](auto ic) __attribute__((always_inline)) {
     constexpr int i = decltype(ic)::value;
-    const int c = min(i, nch - 1) * 16;  // past the end: a repeat, never stored
-    ra[i] = ga[c];
-    rb0[i] = gb0[c];
-    rb1[i] = gb1[c];
+    ra[i] = ga[i * 16];
+    rb0[i] = gb0[i * 16];
+    rb1[i] = gb1[i * 16];
   });
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int ch0 = 0; ch0 < nch; ch0 += kAhead) {
-    static_for(std::make_integer_sequence<int, kAhead>{}, [&](auto ic) __attribute__((always_inline)) {
-      constexpr int i = decltype(ic)::value;
-      const int ch = ch0 + i;
-      if (ch < nch) {
-        constexpr int st = i & 1;  // stage st was last read two chunks ago, before the previous barrier
-        sa[st][slot0] = ra[i];
-        sb[st][slot0] = rb0[i];
-        sb[st][slot1] = rb1[i];
-        lds_barrier();  // the later chunks' loads stay in flight
-        const int c = min(ch + kAhead, nch - 1) * 16;
-        ra[i] = ga[c];
-        rb0[i] = gb0[c];
-        rb1[i] = gb1[c];
-        u32x4 fa[4], fb[4];  // all fragments of the chunk first: one LDS wait, then the MFMA chain
+  static_for(std::make_integer_sequence<int, kNch>{}, [&](auto cc) __attribute__((always_inline)) {
+    constexpr int ch = decltype(cc)::value, i = ch % kAhead;
+    constexpr int st = ch & 1;  // stage st was last read two chunks ago, before the previous barrier
+    sa[st][slot0] = ra[i];
+    sb[st][slot0] = rb0[i];
+    sb[st][slot1] = rb1[i];
+    lds_barrier();  // the later chunks' loads stay in flight
+    if constexpr (ch + kAhead < kNch) {
+      ra[i] = ga[(ch + kAhead) * 16];
+      rb0[i] = gb0[(ch + kAhead) * 16];
+      rb1[i] = gb1[(ch + kAhead) * 16];
+    }
+    u32x4 fa[4], fb[4];  // all fragments of the chunk first: one LDS wait, then the MFMA chain
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          fa[j] = sa[st][(tq * 4 + j) * 64 + lane];
-          fb[j] = sb[st][(eq * 4 + j) * 64 + lane];
-        }
-        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // 8 LDS reads, then 4 MFMAs
-        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    for (int j = 0; j < 4; ++j) {
+      fa[j] = sa[st][(tq * 4 + j) * 64 + lane];
+      fb[j] = sb[st][(eq * 4 + j) * 64 + lane];
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // 8 LDS reads, then 4 MFMAs
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc = mfma16x16x32(__builtin_bit_cast(uint4, fa[j]), __builtin_bit_cast(uint4, fb[j]), acc);
-      }
-    });
-  }
+    for (int j = 0; j < 4; ++j)
+      acc = mfma16x16x32(__builtin_bit_cast(uint4, fa[j]), __builtin_bit_cast(uint4, fb[j]), acc);
+  });
   const int e = e0 + eq * 16 + lr;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -243,23 +248,14 @@ __device__ __forceinline__ void router_big_tile(const uint16_t* __restrict__ x, 
   }
 }
 
-// One launch doing the work that needs no routing: router tiles (optional),
-// activation prep rows, and zeroing of the multi-workgroup routing buffers.
-// block = 512.  blocks: [0, n_router) router tiles, then prep blocks (prep_rows_per_block rows),
-// then n_zero blocks clearing zero_words 32-bit words.
+// One launch doing the work that needs no routing: activation prep rows, zeroing
+// of the multi-workgroup routing buffers, and router tiles (optional).
+// block = 512.  blocks: [0, prep blocks) prep (prep_rows_per_block rows each), then
+// n_zero blocks clearing zero_words 32-bit words, then n_router router tiles.  The
+// short blocks go first: at long T the router tiles fill every CU for most of the
+// launch (one workgroup per CU), and blocks behind them would start only at its end.
 __global__ __launch_bounds__(512) void front_kernel(FrontParams p) {
   int b = blockIdx.x;
-  if (b < p.n_router) {
-    if (p.router_big) {
-      const int tiles_e = (p.E + 63) / 64;
-      router_big_tile(p.x, p.router_w, p.logits, p.T, p.E, p.H, (b / tiles_e) * 32, (b % tiles_e) * 64);
-    } else {
-      const int tiles_e = (p.E + 15) / 16;
-      router_tile(p.x, p.router_w, p.logits, p.T, p.E, p.H, (b / tiles_e) * 16, (b % tiles_e) * 16);
-    }
-    return;
-  }
-  b -= p.n_router;
   const int per_block = prep_rows_per_block(p.prep_rows);
   const int prep_blocks = (p.prep_rows + per_block - 1) / per_block;
   if (b < prep_blocks) {
@@ -268,9 +264,24 @@ __global__ __launch_bounds__(512) void front_kernel(FrontParams p) {
     return;
   }
   b -= prep_blocks;
-  for (int64_t i = static_cast<int64_t>(b) * 512 + threadIdx.x; i < p.zero_words;
-       i += static_cast<int64_t>(p.n_zero) * 512)
-    p.zero[i] = 0u;
+  if (b < p.n_zero) {
+    for (int64_t i = static_cast<int64_t>(b) * 512 + threadIdx.x; i < p.zero_words;
+         i += static_cast<int64_t>(p.n_zero) * 512)
+      p.zero[i] = 0u;
+    return;
+  }
+  b -= p.n_zero;
+  if (p.router_big) {
+    __shared__ RouterLds lds;  // one buffer for every H instance
+    const int tiles_e = (p.E + 63) / 64;
+    const int t0 = (b / tiles_e) * 32, e0 = (b % tiles_e) * 64;
+    if (p.H == 512) router_big_tile<4>(p.x, p.router_w, p.logits, p.T, p.E, t0, e0, lds);
+    else if (p.H == 1024) router_big_tile<8>(p.x, p.router_w, p.logits, p.T, p.E, t0, e0, lds);
+    else router_big_tile<16>(p.x, p.router_w, p.logits, p.T, p.E, t0, e0, lds);
+  } else {
+    const int tiles_e = (p.E + 15) / 16;
+    router_tile(p.x, p.router_w, p.logits, p.T, p.E, p.H, (b / tiles_e) * 16, (b % tiles_e) * 16);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -629,7 +640,7 @@ __global__ __launch_bounds__(64) void combine_kernel(const YT* __restrict__ y, c
 
 // ---------------------------------------------------------------------------
 // host launchers
-bool router_big_fits(int T, int H) { return T >= 64 && H % 128 == 0; }
+bool router_big_fits(int T, int H) { return T >= 64 && (H == 512 || H == 1024 || H == 2048); }
 
 int router_tiles(int T, int E, int H) {
   return router_big_fits(T, H) ? ((T + 31) / 32) * ((E + 63) / 64) : ((T + 15) / 16) * ((E + 15) / 16);

@@ -30,7 +30,7 @@
 // Modes (reference citations):
 //   kModeGateUp : h = silu(x.Wg^T) * (x.Wu^T), bf16, octet-interleaved, and its
 //                 -136*sum per 128 columns for the down GEMM        (reference/fused_ops.py:170-171)
-//   kModeDown   : y = route_weight * (h . Wd^T), fp32              (fused/quantization.py:196-199)
+//   kModeDown   : y = route_weight * (h . Wd^T), rounded to bf16   (fused/quantization.py:196-199)
 #include <type_traits>
 
 #include "kernels.h"
