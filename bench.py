@@ -90,6 +90,38 @@ def weight_sets(pkg, nsets, device, seed=1234, hidden=2048, inter=512, experts=2
     return sets
 
 
+# The target model's quantized non-expert projections and its LM head (graph/quant_plan.py:25-32,55-56),
+# N x K: GDN in_proj_qkv / in_proj_z / in_proj_a|b / out_proj (16 key heads, 32 value heads, head
+# dims 128: fused/ops.py:354-360); attention q (gated) / k|v / o (16 heads, 2 KV heads, head_dim 256).
+QLINEAR_SHAPES = (
+    ("linear_attn.in_proj_qkv", 8192, 2048), ("linear_attn.in_proj_z", 4096, 2048),
+    ("linear_attn.in_proj_a", 32, 2048), ("linear_attn.in_proj_b", 32, 2048),
+    ("linear_attn.out_proj", 2048, 4096),
+    ("self_attn.q_proj", 8192, 2048), ("self_attn.k_proj", 512, 2048), ("self_attn.v_proj", 512, 2048),
+    ("self_attn.o_proj", 2048, 4096),
+    ("lm_head", 248320, 2048),
+)
+
+
+def time_qlinear(pkg, device, steps, warmup, nsets=3, tokens=16):
+    """W4A16 qlinear per projection at a 16-token block: tiled weights, `nsets` rotated copies."""
+    gen = torch.Generator(device=device).manual_seed(4321)
+    x = torch.randn((tokens, 4096), device=device, generator=gen).to(torch.bfloat16)
+    out = {}
+    for name, n, k in QLINEAR_SHAPES:
+        ws_ = [device_bank(pkg, gen, (n, k), device).tiled() for _ in range(nsets)]
+        xk = x[:, :k].contiguous()
+        work = torch.empty(pkg.ops.qlinear_workspace_bytes(tokens, k, 128), dtype=torch.uint8, device=device)
+        ms = time_steps(lambda j: pkg.ops.qlinear(xk, ws_[j % nsets], workspace=work), steps, warmup)
+        nbytes = n * k // 2 + n * (k // 128) * 2
+        out[name] = {"n": n, "k": k, "us": round(ms * 1e3, 2), "weight_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+        del ws_
+    gdn = sum(out[f"linear_attn.{p}"]["us"] for p in ("in_proj_qkv", "in_proj_z", "in_proj_a", "in_proj_b", "out_proj"))
+    attn = sum(out[f"self_attn.{p}"]["us"] for p in ("q_proj", "k_proj", "v_proj", "o_proj"))
+    return {"tokens": tokens, "group_size": 128, "projections": out,
+            "gdn_layer_projections_us": round(gdn, 2), "attention_layer_projections_us": round(attn, 2)}
+
+
 def moe_flops(tokens, k, hidden=2048, inter=512):
     per_row = 2 * (2 * inter * hidden + hidden * inter)
     return per_row * (tokens * k + tokens)
@@ -258,6 +290,7 @@ def main() -> int:
     ap.add_argument("--sets", type=int, default=3, help="independent weight sets rotated per step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-qlinear", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (reference dispatch for HBM byte counters)")
     args = ap.parse_args()
@@ -333,6 +366,9 @@ def main() -> int:
         tflops = moe_flops(2048, top_k) / (ms_p * 1e-3) / 1e12
         result["prefill"] = {"tokens": 2048, "us_per_layer": round(ms_p * 1e3, 1), "tflops": round(tflops, 2),
                              "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4), "steps": steps_p}
+    if not args.no_qlinear:
+        log("timing the qlinear projections and the LM head")
+        result["qlinear"] = time_qlinear(pkg, device, max(24, args.steps // 2), args.warmup)
     if not args.no_cpu_baseline:
         log("timing the CPU baseline")
         result["cpu_baseline"] = cpu_baseline(pkg, tokens, top_k)

@@ -565,15 +565,17 @@ int dflash_qlinear_w4a16(const void* x, int64_t m, const dflash_w4* weight, void
     Carver c;
     uint16_t* x_il = at<uint16_t>(workspace, c.take(2 * static_cast<size_t>(m) * K));
     float* xneg = at<float>(workspace, c.take(4 * static_cast<size_t>(m) * (K / 128)));
-    dflash::FrontParams f{};
-    f.x = static_cast<const uint16_t*>(x);
-    f.T = static_cast<int>(m);
-    f.prep_rows = static_cast<int>(m);
-    f.H = static_cast<int>(K);
-    f.x_il = x_il;
-    f.xneg = xneg;
-    dflash::launch_front(f, st);
-    if (int r = launch_status("prep")) return r;
+    if (!verify) {  // the verify kernel converts the raw rows itself
+      dflash::FrontParams f{};
+      f.x = static_cast<const uint16_t*>(x);
+      f.T = static_cast<int>(m);
+      f.prep_rows = static_cast<int>(m);
+      f.H = static_cast<int>(K);
+      f.x_il = x_il;
+      f.xneg = xneg;
+      dflash::launch_front(f, st);
+      if (int r = launch_status("prep")) return r;
+    }
     dflash::W4StreamParams p{};
     p.w = static_cast<const uint8_t*>(weight->packed);
     p.s = weight->scales;
@@ -587,6 +589,8 @@ int dflash_qlinear_w4a16(const void* x, int64_t m, const dflash_w4* weight, void
     p.out_bf16 = static_cast<uint16_t*>(y);
     p.M = static_cast<int>(m);
     if (verify) {
+      p.act = static_cast<const uint16_t*>(x);
+      p.act_neg = nullptr;
       p.rows_per_pass = 16;
       p.strips = p.N / 32;
       vl.g = p;

@@ -34,7 +34,8 @@
 //             (Combining inside this launch would need an agent-scope release
 //             per workgroup, an L2 write-back on every XCD, which measured
 //             slower than one more launch.)
-//   linear  : x rows of a plain qlinear (one pass per 16 rows).
+//   linear  : the raw x rows of a plain qlinear, converted while staged (one
+//             launch per qlinear); one pass per 16 rows.
 //
 // Semantics per mode (reference citations):
 //   kModeLinear : y = x . dequant(W)^T, bf16 out                 (fused/quantization.py:154-165)
@@ -481,6 +482,45 @@ __device__ __forceinline__ void stage_x(const VerifyParams& vp, char* lds) {
     dma4(nr, lds_neg + i * 64, static_cast<uint32_t>(lane * 4), static_cast<uint32_t>(i * 256));
 }
 
+// Linear mode: the caller's raw bf16 x rows, converted while they are staged (the
+// activation prep the other paths run as a launch of its own): every 16-byte
+// octet to the octet-interleaved order of the MFMA A operand, and -136*sum per
+// 128-column block (per-chunk sums in the prep kernel's order).  A thread issues
+// all of its loads (at most 16) before it uses any.
+template <int kNKB>
+__device__ __forceinline__ void stage_x_raw(const VerifyParams& vp, char* lds) {
+  const W4StreamParams& p = vp.g;
+  constexpr int kK = kNKB * 128, kRS = kK * 2 + 16, kChunks = kK / 8;
+  constexpr int kPer = kNKB < 16 ? kNKB : 16;  // rows * kChunks <= 512 * kPer (M <= 32, or 16 at K = 4096)
+  uint8_t* lds_a = reinterpret_cast<uint8_t*>(lds + vp.lds_a);
+  float* lds_neg = reinterpret_cast<float*>(lds + vp.lds_neg);
+  const int total = p.M * kChunks;
+  const buf_rsrc xr = make_rsrc(p.act, static_cast<uint32_t>(total) * 16);
+  uint4 v[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j)
+    v[j] = buf_load16(xr, static_cast<uint32_t>(threadIdx.x + kVThreads * j) * 16, 0);  // 0 past the rows
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int i = threadIdx.x + kVThreads * j;  // 16-lane rows hold the 16 chunks of one 128-column block
+    if (i < total) {
+      const int r = i / kChunks, c = i - r * kChunks;
+      uint4 o;  // natural pairs (0,1)(2,3)(4,5)(6,7) -> (0,4)(1,5)(2,6)(3,7)
+      o.x = (v[j].x & 0xFFFFu) | (v[j].z << 16);
+      o.y = (v[j].x >> 16) | (v[j].z & 0xFFFF0000u);
+      o.z = (v[j].y & 0xFFFFu) | (v[j].w << 16);
+      o.w = (v[j].y >> 16) | (v[j].w & 0xFFFF0000u);
+      *reinterpret_cast<uint4*>(lds_a + r * kRS + c * 16) = o;
+      const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+      float sum = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) sum += __uint_as_float(w[q] << 16) + __uint_as_float(w[q] & 0xFFFF0000u);
+      sum = row16_sum(sum);
+      if ((c & 15) == 0) lds_neg[r * kNKB + (c >> 4)] = -kDequantOffset * sum;
+    }
+  }
+}
+
 // Passes of the launch.  The gate/up launch routes the block here when asked
 // (its x staging is issued first and stays in flight meanwhile).
 template <int kMode, int kNKB>
@@ -651,7 +691,8 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
             for (int i = tid; i < Pc_end - Pc; i += kVThreads) lds_pdesc[i] = p.pass_table[Pc + i];
             for (int i = tid; i < p.T * p.top_k; i += kVThreads) lds_tok[i] = p.tok[i];
           }
-          stage_x<kMode, kNKB>(vp, lds);
+          if (kMode == kModeLinear) stage_x_raw<kNKB>(vp, lds);
+          else stage_x<kMode, kNKB>(vp, lds);
         }
       } else {
         // down: the chunk's pass descriptors, per pass its 16 h rows (clamped to the slot) and
@@ -808,7 +849,8 @@ __global__ __launch_bounds__(512) void w4_verify_kernel(VerifyParams vp) {
 // ---------------------------------------------------------------------------
 // host side
 bool verify_layout(int mode, int T, int K, int N, int E, int k, int has_shared, int route, VerifyParams* vp) {
-  if (K != 512 && K != 1024 && K != 2048) return false;
+  // K = 4096 (the attention output projections) only as a plain linear: its x rows fill most of the LDS
+  if (K != 512 && K != 1024 && K != 2048 && !(K == 4096 && mode == kModeLinear)) return false;
   if (T <= 0 || T > 32 || k <= 0) return false;
   if (N % (mode == kModeGateUp ? 32 : kVStrip)) return false;
   const int rs = 2 * K + 16, nkb = K / 128;
@@ -888,7 +930,10 @@ void launch_w4_verify(int mode, bool fp32_scales, int grid, const VerifyParams& 
     default: DFLASH_VERIFY(MODE, 16); break;     \
   }
   switch (mode) {
-    case kModeLinear: DFLASH_VERIFY_K(kModeLinear) break;
+    case kModeLinear:
+      if (vp.g.K == 4096) DFLASH_VERIFY(kModeLinear, 32);
+      else DFLASH_VERIFY_K(kModeLinear)
+      break;
     case kModeGateUp: DFLASH_VERIFY_K(kModeGateUp) break;
     default: DFLASH_VERIFY_K(kModeDown) break;
   }

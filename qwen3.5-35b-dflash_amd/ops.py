@@ -232,6 +232,10 @@ def moe_w4a16(hidden: torch.Tensor, gate_up: PackedW4, down: PackedW4, *, top_k:
     return out
 
 
+def qlinear_workspace_bytes(m: int, k: int, group_size: int = 128) -> int:
+    return int(_lib.load().dflash_qlinear_workspace_bytes(m, k, group_size))
+
+
 def moe_workspace_bytes(tokens: int, hidden: int, inter: int, experts: int, top_k: int, group_size: int,
                         has_shared: bool) -> int:
     return int(_lib.load().dflash_moe_workspace_bytes(tokens, hidden, inter, experts, top_k, group_size,

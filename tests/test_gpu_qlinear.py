@@ -43,6 +43,54 @@ def test_qlinear_matches_oracle(pkg, device, m, n, k, group, scale_dtype):
     assert report["cosine"] > 0.9999, report
 
 
+# The target model's quantized projections at a 16-token verify block (graph/quant_plan.py:25-32):
+# GDN in_proj_qkv / in_proj_z / in_proj_a|b / out_proj (32 value heads x 128, 16 key heads x 128,
+# fused/ops.py:354-360), attention q (gated) / k|v / o (head_dim 256), shared expert gate|up / down.
+MODEL_PROJECTIONS = [
+    ("linear_attn.in_proj_qkv", 8192, 2048), ("linear_attn.in_proj_z", 4096, 2048),
+    ("linear_attn.in_proj_a", 32, 2048), ("linear_attn.out_proj", 2048, 4096),
+    ("self_attn.q_proj", 8192, 2048), ("self_attn.k_proj", 512, 2048), ("self_attn.o_proj", 2048, 4096),
+    ("mlp.shared_expert.down_proj", 2048, 512),
+]
+
+
+@pytest.mark.parametrize("name,n,k", MODEL_PROJECTIONS, ids=[p[0] for p in MODEL_PROJECTIONS])
+@pytest.mark.parametrize("layout", ["portable", "tiled"])
+def test_qlinear_model_projections(pkg, device, name, n, k, layout):
+    print(f"qlinear {name} m=16 n={n} k={k} {layout}", flush=True)
+    x, weight = _case(pkg, 16, n, k, 128, torch.bfloat16, seed=n + k)
+    w = weight.to(device)
+    if layout == "tiled":
+        w = w.tiled()
+    y = pkg.ops.qlinear(x.to(device), w).cpu()
+    golden = w4.qlinear(x, weight.packed.numpy(), weight.scales, 128)
+    report = metrics.compare(y, golden)
+    assert report["max_rel"] <= TOL and report["cosine"] > 0.9999, report
+
+
+@pytest.mark.parametrize("m", [5, 16, 24])
+def test_qlinear_k4096_row_counts(pkg, device, m):
+    """K = 4096 runs the verify kernel up to 16 rows and the streaming kernels above."""
+    x, weight = _case(pkg, m, 256, 4096, 128, torch.bfloat16, seed=m)
+    y = pkg.ops.qlinear(x.to(device), weight.to(device)).cpu()
+    report = metrics.compare(y, w4.qlinear(x, weight.packed.numpy(), weight.scales, 128))
+    assert report["max_rel"] <= TOL and report["cosine"] > 0.9999, report
+
+
+def test_qlinear_lm_head(pkg, device):
+    """The LM head [248320, 2048] at a 16-token block: every column on the GPU, a seeded
+    sample of 4096 columns against the oracle (the full oracle product is 8 GMAC)."""
+    n, k, m = 248320, 2048, 16
+    print(f"qlinear lm_head m={m} n={n} k={k}", flush=True)
+    x, weight = _case(pkg, m, n, k, 128, torch.bfloat16, seed=248)
+    y = pkg.ops.qlinear(x.to(device), weight.to(device).tiled()).cpu()
+    assert tuple(y.shape) == (m, n) and torch.isfinite(y.float()).all()
+    cols = torch.randperm(n, generator=torch.Generator().manual_seed(7))[:4096].sort().values
+    golden = w4.qlinear(x, weight.packed[cols].numpy(), weight.scales[cols], 128)
+    report = metrics.compare(y[:, cols], golden)
+    assert report["max_rel"] <= TOL and report["cosine"] > 0.9999, report
+
+
 def test_qlinear_known_answers(pkg, device):
     """One-hot rows pick out a dequantised column; all-ones rows give row sums."""
     n, k, group = 64, 512, 128
