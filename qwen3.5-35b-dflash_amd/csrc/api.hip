@@ -173,8 +173,13 @@ bool moe_tile_path(const MoeShapes& S) {
          w4_tile_supports(kModeDown, static_cast<int>(S.H), static_cast<int>(S.I), static_cast<int>(S.Gd));
 }
 
+bool verify_fits(const MoeShapes& S, bool route, dflash::VerifyParams* gu, dflash::VerifyParams* dn);
+
+// Rows per pass of the work table: 16 on the verify and wave paths (T <= 32), 96 on
+// the prefill tile path, else 16 per token tile of the streaming kernel.
 int rows_per_pass(const MoeShapes& S) {
-  if (moe_wave_path(S)) return 16;
+  dflash::VerifyParams gu, dn;
+  if (verify_fits(S, false, &gu, &dn) || moe_wave_path(S)) return 16;
   if (moe_tile_path(S)) return dflash::kTileRowsPerPass;
   return 16 * token_tiles(S.T);
 }
@@ -268,7 +273,8 @@ bool w4_path_reads_tiled(int mode, int N, int K, int G, GemmPath path) {
 // launch running the combine.  False when the shapes need the other kernels.
 bool verify_fits(const MoeShapes& S, bool route, dflash::VerifyParams* gu, dflash::VerifyParams* dn) {
   using namespace dflash;
-  if (!moe_wave_path(S)) return false;
+  const auto group_ok = [](int64_t g) { return g == 128 || g == 256; };
+  if (S.T > kWaveMaxTokens || S.T * S.k > kWaveMaxTokenRows || !group_ok(S.G) || !group_ok(S.Gd)) return false;
   const int T = static_cast<int>(S.T), H = static_cast<int>(S.H), I = static_cast<int>(S.I);
   const int E = static_cast<int>(S.E), k = static_cast<int>(S.k), sh = S.shared ? 1 : 0;
   *gu = VerifyParams{};
@@ -309,10 +315,10 @@ int run_verify(const MoeShapes& S, dflash::VerifyParams gu, dflash::VerifyParams
   p.w_shared = S.shared ? static_cast<const uint8_t*>(sgu->packed) : nullptr;
   p.s_shared = S.shared ? sgu->scales : nullptr;
   p.w_stride = S.I * S.H;
-  p.s_stride = 2 * S.I * (S.H / 128);
+  p.s_stride = 2 * S.I * (S.H / S.G);
   p.N = 2 * I;
   p.K = H;
-  p.G = 128;
+  p.G = static_cast<int>(S.G);
   p.act = at<uint16_t>(ws, L.x_il);
   p.act_neg = at<float>(ws, L.xneg);
   p.neg_parts = 1;
@@ -345,7 +351,8 @@ int run_verify(const MoeShapes& S, dflash::VerifyParams gu, dflash::VerifyParams
   p.w_shared = S.shared ? static_cast<const uint8_t*>(sdn->packed) : nullptr;
   p.s_shared = S.shared ? sdn->scales : nullptr;
   p.w_stride = S.H * S.I / 2;
-  p.s_stride = S.H * (S.I / 128);
+  p.s_stride = S.H * (S.I / S.Gd);
+  p.G = static_cast<int>(S.Gd);
   p.N = H;
   p.K = I;
   p.act = at<uint16_t>(ws, L.h);
@@ -552,7 +559,7 @@ int dflash_qlinear_w4a16(const void* x, int64_t m, const dflash_w4* weight, void
     // that fit, else the streaming kernel (or its per-wave fallback)
     const bool tiled = weight->layout == DFLASH_LAYOUT_TILED;
     dflash::VerifyParams vl{};
-    const bool verify = weight->group_size == 128 && aligned16(weight->scales) &&
+    const bool verify = (weight->group_size == 128 || weight->group_size == 256) &&
                         dflash::verify_layout(dflash::kModeLinear, static_cast<int>(m), static_cast<int>(K),
                                               static_cast<int>(N), 1, 1, 0, 0, &vl);
     const bool wave = !verify && !tiled && aligned16(weight->scales) &&

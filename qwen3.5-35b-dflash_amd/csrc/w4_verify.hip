@@ -13,8 +13,8 @@
 // timing).
 //
 // Per k-block a lane issues two 16-byte weight loads (16 rows x 64 bytes per
-// tile), 3 k-blocks ahead of the one it computes; a unit's group scales ride
-// with its first k-block (16-byte loads of whole scale rows).  Each k-block is
+// tile) and the two group scales of its rows (group size 128 or 256), ahead of
+// the k-block it computes.  Each k-block is
 // dequantised in registers (bf16 136+q), multiplied on
 // v_mfma_f32_16x16x32_bf16 against A fragments read from LDS, started from
 // -136*sum(a) and scaled.
@@ -575,7 +575,9 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
   // layout's contiguous kilobyte per k-block (tile bases are the same in both)
   const uint32_t wlane = p.tiled ? static_cast<uint32_t>(lane * 16) : static_cast<uint32_t>(lr * rb + kq * 16);
   const uint32_t wkb = p.tiled ? 1024u : 64u;
-  const int slane = p.tiled ? lr : lr * kNKB;  // scale elements: [tile][group][16] or [row][group]
+  // group scales: K / G per row (G = 128 or 256: k-block kb uses group kb >> gshift)
+  const int gshift = p.G == 256 ? 1 : 0, ng = kNKB >> gshift;
+  const int slane = p.tiled ? lr : lr * ng;  // scale elements: [tile][group][16] or [row][group]
   const int skb = p.tiled ? 16 : 1;
 
   const int P_first = ub / strips, P_last = ue > ub ? (ue - 1) / strips : P_first - 1;
@@ -656,7 +658,7 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
                                (shared ? 0 : e * p.s_stride * static_cast<int64_t>(sizeof(ScaleT)));
         const int64_t row0 = static_cast<int64_t>(strip) * kTileRows;
         l_w = wbase + row0 * rb;
-        l_s = sbase + row0 * kNKB * static_cast<int64_t>(sizeof(ScaleT));
+        l_s = sbase + row0 * ng * static_cast<int64_t>(sizeof(ScaleT));
       };
       // ring of k-blocks in flight: two 16-byte weight loads and the two group scales of the lane's rows
       uint4 wbuf[kVDepth][2];
@@ -672,9 +674,9 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
         }
         dst[0] = *reinterpret_cast<const uint4*>(l_w + wlane + kb * wkb);
         dst[1] = *reinterpret_cast<const uint4*>(l_w + second * rb + wlane + kb * wkb);
-        const ScaleT* sp = reinterpret_cast<const ScaleT*>(l_s) + slane + kb * skb;
+        const ScaleT* sp = reinterpret_cast<const ScaleT*>(l_s) + slane + (kb >> gshift) * skb;
         sdst[0] = load_scale_bits(sp);
-        sdst[1] = load_scale_bits(sp + second * kNKB);
+        sdst[1] = load_scale_bits(sp + second * ng);
         ++lg;
       };
       // the first k-blocks go out before the activations are staged (they do not depend on them)

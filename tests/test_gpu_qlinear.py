@@ -31,6 +31,8 @@ def _case(pkg, m, n, k, group, scale_dtype, seed):
     (16, 2048, 512, 128, torch.bfloat16),
     (32, 64, 1024, 128, torch.float32),
     (24, 128, 2048, 128, torch.float32),
+    (16, 512, 2048, 256, torch.float32),    # the reference quantizer's g256 fp32 scales, verify kernel
+    (16, 256, 4096, 256, torch.bfloat16),   # g256 at K = 4096
 ])
 def test_qlinear_matches_oracle(pkg, device, m, n, k, group, scale_dtype):
     print(f"qlinear m={m} n={n} k={k} g={group} {scale_dtype}", flush=True)

@@ -75,6 +75,7 @@ def _banks(pkg, layer, device, tiled):
     (128, 256, 8, 2048, 512, 128, torch.bfloat16, True),   # streaming kernel, skewed routing
     (300, 16, 4, 1024, 512, 128, torch.float32, False),    # prefill tile kernel, fp32 scales
     (256, 8, 2, 2048, 512, 256, torch.bfloat16, False),    # prefill tile kernel, group 256
+    (16, 256, 8, 2048, 512, 256, torch.float32, False),   # verify block, group 256 fp32 scales
 ])
 def test_moe_tiled_equals_portable(pkg, device, tokens, experts, k, hidden, inter, group, scale_dtype, skew):
     print(f"moe tiled T={tokens} E={experts} k={k} H={hidden} I={inter} g={group} {scale_dtype} skew={skew}",
