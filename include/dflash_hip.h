@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define DFLASH_ABI_VERSION 2
+#define DFLASH_ABI_VERSION 3
 
 enum dflash_status {
   DFLASH_OK = 0,
@@ -38,7 +38,7 @@ enum dflash_status {
   DFLASH_ERR_HIP = 4               /* a HIP runtime call or kernel launch failed */
 };
 
-enum dflash_dtype { DFLASH_DTYPE_BF16 = 0, DFLASH_DTYPE_F32 = 1 };
+enum dflash_dtype { DFLASH_DTYPE_BF16 = 0, DFLASH_DTYPE_F32 = 1, DFLASH_DTYPE_F16 = 2 /* source scales only */ };
 
 /*
  * Byte order of a packed bank (same sizes either way):
@@ -75,6 +75,24 @@ typedef struct dflash_w4 {
  * CPU reference.  Constraints: rows % 16 == 0, cols % 128 == 0.
  */
 int dflash_w4_to_tiled(const dflash_w4* src, void* packed_out, void* scales_out, void* stream);
+
+/*
+ * Pack weights carried as one signed int8 per int4 value -- the original
+ * checkpoint's format read by target/original_quant.py:214-272 (values int8
+ * [experts][rows][cols] in [-8, 7]; group scales [experts][rows][cols/group_size]
+ * in scales_dtype, fp16 or fp32 there, bf16 accepted too; a linear's trailing
+ * [.., 1] axis is the same memory) -- into a bank in `layout` order with fp32 scales:
+ * packed_out experts*rows*cols/2 bytes, scales_out experts*rows*cols/group_size
+ * floats.  The reference packs the same values into its vendor layout instead
+ * (pack_i4zn, :80-112).  invalid: two device int32 the call clears and fills with
+ * the number of values outside [-8, 7] and of scales that are negative or not
+ * finite (the reader's ValueError cases); they are valid once the stream reaches
+ * them.  Constraints: cols % 32 == 0, group_size in {128, 256}, cols % group_size
+ * == 0; TILED also rows % 16 == 0 and cols % 128 == 0.
+ */
+int dflash_w4_from_int8(const int8_t* values, const void* scales, int32_t scales_dtype, int64_t experts,
+                        int64_t rows, int64_t cols, int64_t group_size, int32_t layout, void* packed_out,
+                        float* scales_out, int32_t* invalid, void* stream);
 
 /* ABI version of the loaded library (DFLASH_ABI_VERSION). */
 int dflash_abi_version(void);

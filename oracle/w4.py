@@ -140,3 +140,30 @@ def from_tiled(packed: np.ndarray, scales: np.ndarray) -> tuple[np.ndarray, np.n
     s = scales.reshape(*lead, n // 16, groups, 16)
     portable_s = np.swapaxes(s, -1, -2).reshape(scales.shape)
     return np.ascontiguousarray(portable), np.ascontiguousarray(portable_s)
+
+
+def from_int8(values: np.ndarray, scales: np.ndarray, *, tiled: bool) -> tuple[np.ndarray, np.ndarray]:
+    """The original checkpoint's int8-carried int4 ``values [..., N, K]`` and group
+    ``scales [..., N, K/G]`` (fp16/fp32; a linear's trailing ``[.., 1]`` axis dropped)
+    -> ``(packed uint8 [..., N, K/2], scales float32)``, in the tiled order when asked.
+
+    Follows the checks of ``target/original_quant.py:252-272`` (values in [-8, 7],
+    scales finite and nonnegative, same messages); the packing is ``pack`` (the same
+    nibble order the reader's I4ZN packer uses inside each byte, ``:107-109``) and the
+    scale widening is exact.  Pinned by its parts: ``pack``, ``to_tiled``, and the
+    ``unpack`` round trip in the tests.
+    """
+    values = np.asarray(values)
+    scales = np.asarray(scales)
+    if values.dtype != np.int8:
+        raise ValueError("logical original quantized weights must have dtype int8")
+    if np.any(values < -8) or np.any(values > 7):
+        raise ValueError("original quantized weight contains values outside signed I4 [-8,7]")
+    if scales.ndim == values.ndim + 1 and scales.shape[-1] == 1:
+        scales = scales[..., 0]
+    wide = scales.astype(np.float32)
+    if not np.isfinite(wide).all() or np.any(wide < 0):
+        raise ValueError("original quantization scales must be finite and nonnegative")
+    packed = pack(values)
+    return to_tiled(packed, wide) if tiled else (packed, wide)
+

@@ -12,9 +12,10 @@ from pathlib import Path
 PACKAGE_DIR = Path(__file__).resolve().parent
 LIBRARY_PATH = PACKAGE_DIR / "libdflash_hip.so"
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 DTYPE_BF16 = 0
 DTYPE_F32 = 1
+DTYPE_F16 = 2
 LAYOUT_PORTABLE = 0
 LAYOUT_TILED = 1
 
@@ -51,6 +52,8 @@ _W4P = ctypes.POINTER(W4Desc)
 SIGNATURES = {
     "dflash_abi_version": (ctypes.c_int, []),
     "dflash_w4_to_tiled": (ctypes.c_int, [_W4P, _P, _P, _P]),
+    "dflash_w4_from_int8": (ctypes.c_int, [_P, _P, ctypes.c_int32, _I64, _I64, _I64, _I64, ctypes.c_int32, _P, _P,
+                                           _P, _P]),
     "dflash_last_error": (ctypes.c_char_p, []),
     "dflash_qlinear_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
     "dflash_qlinear_w4a16": (ctypes.c_int, [_P, _I64, _W4P, _P, _P, _SZ, _P]),

@@ -529,6 +529,38 @@ int dflash_w4_to_tiled(const dflash_w4* src, void* packed_out, void* scales_out,
   }
 }
 
+int dflash_w4_from_int8(const int8_t* values, const void* scales, int32_t scales_dtype, int64_t experts,
+                        int64_t rows, int64_t cols, int64_t group_size, int32_t layout, void* packed_out,
+                        float* scales_out, int32_t* invalid, void* stream) {
+  try {
+    if (experts <= 0 || rows <= 0 || cols <= 0)
+      return fail(DFLASH_ERR_INVALID_ARGUMENT, "from_int8: experts, rows and cols must be positive");
+    if (group_size != 128 && group_size != 256)
+      return fail(DFLASH_ERR_UNSUPPORTED, "from_int8: group_size must be 128 or 256");
+    if (cols % 32 || cols % group_size)
+      return fail(DFLASH_ERR_UNSUPPORTED, "from_int8: cols must be a multiple of 32 and of group_size");
+    if (layout != DFLASH_LAYOUT_PORTABLE && layout != DFLASH_LAYOUT_TILED)
+      return fail(DFLASH_ERR_INVALID_ARGUMENT, "from_int8: unknown layout");
+    if (layout == DFLASH_LAYOUT_TILED && (rows % 16 || cols % 128))
+      return fail(DFLASH_ERR_INVALID_ARGUMENT, "from_int8: the tiled layout needs rows % 16 == 0 and cols % 128 == 0");
+    if (scales_dtype != DFLASH_DTYPE_BF16 && scales_dtype != DFLASH_DTYPE_F32 && scales_dtype != DFLASH_DTYPE_F16)
+      return fail(DFLASH_ERR_INVALID_ARGUMENT, "from_int8: unknown scales_dtype");
+    if (!values || !scales || !packed_out || !scales_out || !invalid)
+      return fail(DFLASH_ERR_INVALID_ARGUMENT, "from_int8: NULL pointer");
+    if (!aligned16(values) || !aligned16(packed_out) || reinterpret_cast<uintptr_t>(scales) % 4 ||
+        reinterpret_cast<uintptr_t>(scales_out) % 4 || reinterpret_cast<uintptr_t>(invalid) % 4)
+      return fail(DFLASH_ERR_INVALID_ARGUMENT, "from_int8: values/packed_out need 16-byte, scales/invalid 4-byte alignment");
+    if (rows > (1 << 30) || cols > (1 << 30) || experts * rows * cols > (int64_t(1) << 40))
+      return fail(DFLASH_ERR_UNSUPPORTED, "from_int8: bank too large");
+    dflash::launch_from_int8(values, scales, scales_dtype, experts, static_cast<int>(rows), static_cast<int>(cols),
+                             static_cast<int>(group_size), layout == DFLASH_LAYOUT_TILED, packed_out, scales_out,
+                             invalid, static_cast<hipStream_t>(stream));
+    return launch_status("from_int8");
+  } catch (...) {
+    return fail(DFLASH_ERR_HIP, "unexpected host exception");
+  }
+}
+
 const char* dflash_last_error(void) { return g_last_error.c_str(); }
 
 size_t dflash_qlinear_workspace_bytes(int64_t m, int64_t k, int64_t group_size) {

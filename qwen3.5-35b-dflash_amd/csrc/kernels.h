@@ -129,6 +129,12 @@ struct W4StreamParams {
 // Portable -> tiled repack of a packed bank and its scales (repack.hip).
 void launch_tile_w4(const void* packed, const void* scales, bool fp32_scales, int64_t experts, int rows, int cols,
                     int group, void* packed_out, void* scales_out, hipStream_t stream);
+// int8-carried int4 values [experts][rows][cols] and group scales (dflash_dtype src) -> packed
+// bank (portable or tiled) with fp32 scales; bad[0] / bad[1] count values outside [-8, 7] /
+// negative or non-finite scales (cleared by the launch).
+void launch_from_int8(const int8_t* values, const void* scales, int scales_dtype, int64_t experts, int rows,
+                      int cols, int group, bool tiled, void* packed_out, float* scales_out, int32_t* bad,
+                      hipStream_t stream);
 
 void launch_front(const FrontParams& p, hipStream_t stream);
 // Router tiles of a launch: 32 tokens x 64 experts when T >= 64 and H % 128 == 0, else 16 x 16.

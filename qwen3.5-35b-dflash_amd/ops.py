@@ -67,6 +67,45 @@ def _workspace(nbytes: int, device: torch.device, workspace: Optional[torch.Tens
     return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
 
 
+_SOURCE_SCALE_DTYPES = {torch.float32: _lib.DTYPE_F32, torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16}
+
+
+def from_int8(values: torch.Tensor, scales: torch.Tensor, group_size: int, *, layout: str = "tiled") -> PackedW4:
+    """Pack the original checkpoint's int8-carried int4 weights into a bank with fp32 scales.
+
+    ``values`` int8 ``[N, K]`` or ``[E, N, K]`` in [-8, 7]; ``scales`` fp16/fp32/bf16
+    ``[..., N, K/G]`` (a linear's ``[N, K/G, 1]`` is accepted, as the reference's
+    reader stores it: ``target/original_quant.py:214-240``).  Raises ``ValueError``
+    with the reader's messages for values outside [-8, 7] and for negative or
+    non-finite scales (``:252-272``); synchronises the stream to check them, as a
+    load-time step.
+    """
+    device = _require_device(values, scales)
+    if values.dtype != torch.int8 or values.ndim not in (2, 3):
+        raise ValueError("original quantized weights must be int8 [N, K] or [E, N, K]")
+    if layout not in ("portable", "tiled"):
+        raise ValueError("layout must be 'portable' or 'tiled'")
+    *lead, n, k = values.shape
+    if k % group_size:
+        raise ValueError(f"K={k} is not a multiple of group_size={group_size}")
+    sc = scales.reshape(*scales.shape[:-1]) if scales.ndim == values.ndim + 1 and scales.shape[-1] == 1 else scales
+    if tuple(sc.shape) != (*lead, n, k // group_size) or sc.dtype not in _SOURCE_SCALE_DTYPES:
+        raise ValueError(f"scales must be fp16/fp32/bf16 [{', '.join(map(str, (*lead, n, k // group_size)))}]")
+    vals, sc = values.contiguous(), sc.contiguous()
+    packed = torch.empty((*lead, n, k // 2), dtype=torch.uint8, device=device)
+    out_scales = torch.empty((*lead, n, k // group_size), dtype=torch.float32, device=device)
+    invalid = torch.empty(2, dtype=torch.int32, device=device)
+    _lib.call("dflash_w4_from_int8", _ptr(vals), _ptr(sc), _SOURCE_SCALE_DTYPES[sc.dtype], lead[0] if lead else 1,
+              n, k, group_size, _lib.LAYOUT_TILED if layout == "tiled" else _lib.LAYOUT_PORTABLE, _ptr(packed),
+              _ptr(out_scales), _ptr(invalid), _stream(device))
+    bad_values, bad_scales = (int(v) for v in invalid.cpu())
+    if bad_values:
+        raise ValueError("original quantized weight contains values outside signed I4 [-8,7]")
+    if bad_scales:
+        raise ValueError("original quantization scales must be finite and nonnegative")
+    return PackedW4(packed, out_scales, group_size, layout)
+
+
 def to_tiled(w: PackedW4) -> PackedW4:
     """Repack a portable bank into the tiled layout (new tensors, same shapes, on w's device)."""
     w.validate("weight")

@@ -28,7 +28,7 @@ def test_library_loads_and_exports_every_symbol(pkg):
     lib = pkg._lib.load()
     for name in _declared_functions():
         assert hasattr(lib, name), name
-    assert lib.dflash_abi_version() == pkg._lib.ABI_VERSION == 2
+    assert lib.dflash_abi_version() == pkg._lib.ABI_VERSION == 3
 
 
 def test_library_has_no_unresolved_internal_symbols(pkg):
@@ -110,6 +110,33 @@ def test_to_tiled_validation(pkg):
     assert st == 1 and "alias" in msg
     st, msg = _status(pkg, "dflash_w4_to_tiled", ctypes.byref(d), ctypes.c_void_p((1 << 20) + 8), out, None)
     assert st == 1 and "aligned" in msg
+
+
+def test_from_int8_validation(pkg):
+    """The int8-carried repack validates shapes, layout, dtypes and pointers before any launch."""
+    v = ctypes.c_void_p(1 << 20)
+    bad = ctypes.c_void_p(1 << 21)
+
+    def call(experts=1, rows=512, cols=2048, group=256, dtype=1, layout=1, values=v, invalid=bad):
+        return _status(pkg, "dflash_w4_from_int8", values, v, dtype, experts, rows, cols, group, layout, v, v,
+                       invalid, None)
+
+    st, msg = call(group=64)
+    assert st == 2 and "group_size" in msg
+    st, msg = call(cols=2048 + 16)
+    assert st == 2 and "multiple of 32" in msg
+    st, msg = call(rows=40)
+    assert st == 1 and "rows % 16" in msg
+    st, msg = call(layout=7)
+    assert st == 1 and "layout" in msg
+    st, msg = call(dtype=9)
+    assert st == 1 and "scales_dtype" in msg
+    st, msg = call(values=None)
+    assert st == 1 and "NULL" in msg
+    st, msg = call(values=ctypes.c_void_p((1 << 20) + 8))
+    assert st == 1 and "alignment" in msg
+    st, msg = call(experts=0)
+    assert st == 1 and "positive" in msg
 
 
 @host_only

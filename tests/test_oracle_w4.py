@@ -125,3 +125,37 @@ def test_to_tiled_follows_the_bytewise_definition(lead, n, k, groups):
 def test_to_tiled_rejects_untileable_shapes():
     with pytest.raises(ValueError):
         w4.to_tiled(np.zeros((24, 64), np.uint8), np.zeros((24, 1), np.float32))
+
+
+def test_from_int8_round_trips_and_widens_scales_exactly():
+    """The int8-carried reader format: packing then unpacking returns the values, the
+    tiled order is the bytewise to_tiled, fp16 scales widen exactly, the trailing
+    [.., 1] scale axis of a linear is dropped."""
+    rng = np.random.default_rng(3)
+    values = rng.integers(-8, 8, size=(2, 32, 512), dtype=np.int8)
+    scales = (rng.random((2, 32, 2)) * 0.02).astype(np.float16)
+    packed, wide = w4.from_int8(values, scales, tiled=False)
+    np.testing.assert_array_equal(w4.unpack(packed), values)
+    assert wide.dtype == np.float32 and np.array_equal(wide, scales.astype(np.float32))
+    tp, ts = w4.from_int8(values, scales, tiled=True)
+    ep, es = w4.to_tiled(packed, wide)
+    np.testing.assert_array_equal(tp, ep)
+    np.testing.assert_array_equal(ts, es)
+    lp, ls = w4.from_int8(values[0], scales[0][..., None], tiled=False)
+    np.testing.assert_array_equal(lp, packed[0])
+    np.testing.assert_array_equal(ls, wide[0])
+
+
+@pytest.mark.parametrize("case", ["value", "negative", "nan", "inf"])
+def test_from_int8_rejects_what_the_reader_rejects(case):
+    values = np.zeros((16, 256), dtype=np.int8)
+    scales = np.ones((16, 1), dtype=np.float32)
+    if case == "value":
+        values[3, 7] = 8
+        match = "outside signed I4"
+    else:
+        scales[5, 0] = {"negative": -1.0, "nan": np.nan, "inf": np.inf}[case]
+        match = "finite and nonnegative"
+    with pytest.raises(ValueError, match=match):
+        w4.from_int8(values, scales, tiled=False)
+
