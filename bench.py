@@ -118,8 +118,21 @@ def time_qlinear(pkg, device, steps, warmup, nsets=3, tokens=16):
         del ws_
     gdn = sum(out[f"linear_attn.{p}"]["us"] for p in ("in_proj_qkv", "in_proj_z", "in_proj_a", "in_proj_b", "out_proj"))
     attn = sum(out[f"self_attn.{p}"]["us"] for p in ("q_proj", "k_proj", "v_proj", "o_proj"))
-    return {"tokens": tokens, "group_size": 128, "projections": out,
-            "gdn_layer_projections_us": round(gdn, 2), "attention_layer_projections_us": round(attn, 2)}
+    # projections reading the same x stacked into one matrix (pkg.concat_rows): one launch each
+    stacked = {}
+    for name, n in (("linear_attn.in_proj_qkv+z+a+b", 8192 + 4096 + 32 + 32), ("self_attn.q+k+v_proj", 8192 + 512 + 512)):
+        ws_ = [device_bank(pkg, gen, (n, 2048), device).tiled() for _ in range(nsets)]
+        xk = x[:, :2048].contiguous()
+        work = torch.empty(pkg.ops.qlinear_workspace_bytes(tokens, 2048, 128), dtype=torch.uint8, device=device)
+        ms = time_steps(lambda j: pkg.ops.qlinear(xk, ws_[j % nsets], workspace=work), steps, warmup)
+        stacked[name] = {"n": n, "k": 2048, "us": round(ms * 1e3, 2)}
+        del ws_
+    gdn_s = stacked["linear_attn.in_proj_qkv+z+a+b"]["us"] + out["linear_attn.out_proj"]["us"]
+    attn_s = stacked["self_attn.q+k+v_proj"]["us"] + out["self_attn.o_proj"]["us"]
+    return {"tokens": tokens, "group_size": 128, "projections": out, "stacked": stacked,
+            "gdn_layer_projections_us": round(gdn, 2), "attention_layer_projections_us": round(attn, 2),
+            "gdn_layer_projections_stacked_us": round(gdn_s, 2),
+            "attention_layer_projections_stacked_us": round(attn_s, 2)}
 
 
 def moe_flops(tokens, k, hidden=2048, inter=512):

@@ -12,4 +12,4 @@ The directory name is not a Python identifier; load it under the alias
 * ``build``     -- hipcc build recipe
 """
 from . import _lib, fused_ops, ops, packing, synthetic  # noqa: F401
-from .packing import PackedW4, SharedExpert, pack_int4, quantize_w4  # noqa: F401
+from .packing import PackedW4, SharedExpert, concat_rows, pack_int4, quantize_w4  # noqa: F401

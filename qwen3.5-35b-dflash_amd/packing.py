@@ -76,6 +76,31 @@ class PackedW4(NamedTuple):
         return to_tiled(self)
 
 
+def concat_rows(*banks: PackedW4) -> PackedW4:
+    """Matrices ``[N_i, K]`` that read the same activations, stacked into one ``[sum N_i, K]``
+    so a single qlinear launch computes all of them (split its output at the ``N_i``).
+
+    The tiled layout orders bytes per 16-row tile, so stacking tiled matrices whose row
+    counts are multiples of 16 is a plain concatenation of their bytes and scales, like
+    the portable one.  Every output column is computed from its own weight row as in a
+    separate call; only the order in which a column's k-block partial sums are added can
+    differ (the kernels split each workgroup's share of the stacked matrix over its waves),
+    so results agree to fp32 rounding before the one bf16 rounding.
+    """
+    if not banks:
+        raise ValueError("concat_rows needs at least one matrix")
+    first = banks[0]
+    for i, b in enumerate(banks):
+        b.validate(f"bank {i}")
+        if b.packed.ndim != 2:
+            raise ValueError("concat_rows stacks 2-D matrices [N, K/2]")
+        if (b.cols, b.group_size, b.layout, b.scales.dtype, b.packed.device) != (
+                first.cols, first.group_size, first.layout, first.scales.dtype, first.packed.device):
+            raise ValueError("concat_rows needs one K, group size, layout, scale dtype and device")
+    return PackedW4(torch.cat([b.packed for b in banks]).contiguous(), torch.cat([b.scales for b in banks]).contiguous(),
+                    first.group_size, first.layout)
+
+
 class SharedExpert(NamedTuple):
     """Always-on shared expert: gate/up rows stacked ``[2I, H]``, down ``[H, I]``, gate vector ``[H]``.
 

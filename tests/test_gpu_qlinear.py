@@ -70,6 +70,31 @@ def test_qlinear_model_projections(pkg, device, name, n, k, layout):
     assert report["max_rel"] <= TOL and report["cosine"] > 0.9999, report
 
 
+@pytest.mark.parametrize("layout", ["portable", "tiled"])
+def test_qlinear_stacked_projections(pkg, device, layout):
+    """The GDN input projections (qkv, z, a, b) stacked into one matrix: one launch; every part
+    within the bar of the oracle and of its separate call (the k-block partial sums of a column
+    may be added in another order, so bits can differ)."""
+    parts = [("qkv", 8192), ("z", 4096), ("a", 32), ("b", 32)]
+    gen = torch.Generator().manual_seed(21)
+    x = torch.randn((16, 2048), generator=gen).to(torch.bfloat16)
+    host = [pkg.synthetic.int4_weight(gen, (n, 2048), 128) for _, n in parts]
+    banks = [h.to(device) for h in host]
+    if layout == "tiled":
+        banks = [b.tiled() for b in banks]
+    stacked = pkg.concat_rows(*banks)
+    assert stacked.layout == layout and stacked.rows == sum(n for _, n in parts)
+    y = pkg.ops.qlinear(x.to(device), stacked).cpu()
+    col = 0
+    for (name, n), h, b in zip(parts, host, banks):
+        part = y[:, col:col + n]
+        golden = w4.qlinear(x, h.packed.numpy(), h.scales, 128)
+        assert metrics.compare(part, golden)["max_rel"] <= TOL, name
+        separate = pkg.ops.qlinear(x.to(device), b).cpu()
+        assert metrics.compare(part, separate)["max_rel"] <= TOL, name
+        col += n
+
+
 @pytest.mark.parametrize("m", [5, 16, 24])
 def test_qlinear_k4096_row_counts(pkg, device, m):
     """K = 4096 runs the verify kernel up to 16 rows and the streaming kernels above."""
