@@ -94,9 +94,12 @@ RouteLayout route_layout(int64_t T, int64_t k, int64_t E) {
   return L;
 }
 
+// The down plan of the verify path covers persistent grids up to this many workgroups.
+constexpr int kDownPlanMaxGrid = 1024;
+
 struct MoeLayout {
   RouteLayout route;
-  size_t logits, x_il, xneg, gate, h, hpart, y, total;
+  size_t logits, x_il, xneg, gate, h, hpart, y, down_plan, total;
 };
 
 MoeLayout moe_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, bool shared) {
@@ -112,6 +115,7 @@ MoeLayout moe_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, bool
   L.h = c.take(2 * rows * I);
   L.hpart = c.take(4 * rows * (I / 16));
   L.y = c.take(4 * rows * H);
+  L.down_plan = c.take(48 * static_cast<size_t>(kDownPlanMaxGrid));
   L.total = c.off;
   return L;
 }
@@ -342,7 +346,14 @@ int run_verify(const MoeShapes& S, dflash::VerifyParams gu, dflash::VerifyParams
     gu.slot_w_out = at<float>(ws, L.route.slot_w);
     gu.tok_out = at<int32_t>(ws, L.route.tok);
   }
-  if (stage_on(DFLASH_STAGE_GATE_UP)) launch_w4_verify(kModeGateUp, S.gu_f32, cu_count(), gu, stream);
+  // the routing gate/up launch also plans the down launch's prologue (same workspace, next launch)
+  const int grid = cu_count();
+  if (gu.route && grid <= kDownPlanMaxGrid) {
+    gu.down_plan = at<int4>(ws, L.down_plan);
+    gu.down_grid = grid;
+    gu.down_strips = H / 32;
+  }
+  if (stage_on(DFLASH_STAGE_GATE_UP)) launch_w4_verify(kModeGateUp, S.gu_f32, grid, gu, stream);
   if (int r = launch_status("gate_up")) return r;
 
   // down: N = H rows over K = I, routing-weight epilogue into y, then the combine
@@ -366,7 +377,10 @@ int run_verify(const MoeShapes& S, dflash::VerifyParams gu, dflash::VerifyParams
   p.strips = H / 32;
   dn.g = p;
   dn.E = static_cast<int>(S.E);
-  if (stage_on(DFLASH_STAGE_DOWN)) launch_w4_verify(kModeDown, S.dn_f32, cu_count(), dn, stream);
+  // a plan exists only when this call's gate/up launch wrote one (measurement mode timing the
+  // down launch alone keeps the work table's pass count)
+  dn.down_plan = gu.down_plan && stage_on(DFLASH_STAGE_GATE_UP) ? gu.down_plan : nullptr;
+  if (stage_on(DFLASH_STAGE_DOWN)) launch_w4_verify(kModeDown, S.dn_f32, grid, dn, stream);
   if (int r = launch_status("down")) return r;
 
   if (measuring()) return DFLASH_OK;
@@ -743,7 +757,7 @@ int dflash_moe_experts_w4a16(const void* hidden, int64_t tokens, int64_t hidden_
     t.xneg = at<float>(workspace, L.xneg);
     t.gate_w = S.shared ? static_cast<const uint16_t*>(shared_gate_weight) : nullptr;
     t.gate_out = at<float>(workspace, L.gate);
-    dflash::VerifyParams vgu, vdn;
+    dflash::VerifyParams vgu{}, vdn{};
     const bool verify = verify_fits(S, false, &vgu, &vdn);
     if (int r = check_tiled_moe(S, verify)) return r;
     if (!measuring()) dflash::launch_table_prep(t, st);
@@ -782,7 +796,7 @@ int dflash_moe_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, co
     const int T = static_cast<int>(S.T), E = static_cast<int>(S.E);
     const bool small = dflash::route_small_fits(T, E, static_cast<int>(S.k));
     // the verify path routes inside its gate/up launch when the block fits there
-    dflash::VerifyParams vgu, vdn;
+    dflash::VerifyParams vgu{}, vdn{};
     const bool verify = tokens > 0 && small && verify_fits(S, true, &vgu, &vdn);
     if (int r = check_tiled_moe(S, verify)) return r;
     float* logits = router_logits ? const_cast<float*>(router_logits)

@@ -192,6 +192,11 @@ struct VerifyParams {
   int4* pass_table_out;
   float* slot_w_out;
   int32_t* tok_out;
+  // down plan: 3 int4 per down workgroup (pass count and first pass; the descriptors of its
+  // first two passes), written by workgroup 0 of a routing gate/up launch, read by the down
+  // launch (null: neither).  down_grid / down_strips: the down launch's grid and strips.
+  int4* down_plan;
+  int down_grid, down_strips;
 };
 // LDS bytes and layout of one verify launch; false when it does not fit (the
 // caller keeps the separate routing / wave-streaming kernels then).

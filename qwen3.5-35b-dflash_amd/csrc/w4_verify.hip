@@ -521,6 +521,22 @@ __device__ __forceinline__ void stage_x_raw(const VerifyParams& vp, char* lds) {
   }
 }
 
+// Workgroup 0 of a gate/up launch that routed the block: the down launch's plan per
+// workgroup b (its pass count and the descriptors of the first two passes of its unit
+// range, 3 int4), so the down prologue needs one load before its first weights.
+__device__ __forceinline__ void write_down_plan(const VerifyParams& vp, const int4* pdesc, int total) {
+  if (!vp.down_plan || blockIdx.x != 0 || total <= 0) return;
+  const int64_t units = static_cast<int64_t>(total) * vp.down_strips;
+  for (int b = threadIdx.x; b < vp.down_grid; b += kVThreads) {
+    const int ub = static_cast<int>(units * b / vp.down_grid);
+    const int P0 = min(ub / vp.down_strips, total - 1), P1 = min(P0 + 1, total - 1);
+    int4* o = vp.down_plan + 3 * b;
+    o[0] = make_int4(total, P0, 0, 0);
+    o[1] = pdesc[P0];
+    o[2] = pdesc[P1];
+  }
+}
+
 // Passes of the launch.  The gate/up launch routes the block here when asked
 // (its x staging is issued first and stays in flight meanwhile).
 template <int kMode, int kNKB>
@@ -531,17 +547,24 @@ __device__ __forceinline__ int verify_passes(const VerifyParams& vp, char* lds) 
     if (vp.E <= 128) {
       const RowKeys<4> keys = route_rows_load<4>(vp);
       stage_x<kMode, kNKB>(vp, lds);
-      return route_rows<4>(vp, keys, lds, lds_pdesc, lds_tok);
+      const int total = route_rows<4>(vp, keys, lds, lds_pdesc, lds_tok);
+      write_down_plan(vp, lds_pdesc, total);
+      return total;
     }
     const RowKeys<8> keys = route_rows_load<8>(vp);
     stage_x<kMode, kNKB>(vp, lds);
-    return route_rows<8>(vp, keys, lds, lds_pdesc, lds_tok);
+    const int total = route_rows<8>(vp, keys, lds, lds_pdesc, lds_tok);
+    write_down_plan(vp, lds_pdesc, total);
+    return total;
   }
   if (kMode == kModeGateUp && vp.route) {
     stage_x<kMode, kNKB>(vp, lds);
-    return route_block(vp, lds, lds_pdesc, lds_tok);
+    const int total = route_block(vp, lds, lds_pdesc, lds_tok);
+    write_down_plan(vp, lds_pdesc, total);
+    return total;
   }
   if (kMode == kModeLinear) return (vp.g.M + 15) >> 4;
+  if (kMode == kModeDown && vp.down_plan) return ld_const_int4(vp.down_plan, 3 * static_cast<int>(blockIdx.x)).x;
   return ld_const(vp.g.meta, 1);
 }
 
@@ -581,6 +604,18 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
   const int skb = p.tiled ? 16 : 1;
 
   const int P_first = ub / strips, P_last = ue > ub ? (ue - 1) / strips : P_first - 1;
+  // down with a plan: the descriptors of the first two passes came with the pass count
+  int plan_p = -2;
+  int4 plan_d0 = make_int4(0, 0, 0, 0), plan_d1 = plan_d0;
+  if (kMode == kModeDown && vp.down_plan) {
+    const int b3 = 3 * static_cast<int>(blockIdx.x);
+    plan_p = ld_const_int4(vp.down_plan, b3).y;
+    plan_d0 = ld_const_int4(vp.down_plan, b3 + 1);
+    plan_d1 = ld_const_int4(vp.down_plan, b3 + 2);
+  }
+  auto early_desc = [&](int P) -> int4 {
+    return P == plan_p ? plan_d0 : P == plan_p + 1 ? plan_d1 : ld_const_int4(p.pass_table, P);
+  };
   // pass descriptors: all of them after in-kernel routing, else the chunk's (staged below)
   int pd_base = 0;
   auto pass_desc = [&](int P) -> int4 {
@@ -650,7 +685,7 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
         // before the staging barrier the descriptor comes from the work table (s_load),
         // except after in-kernel routing, whose table is only in LDS
         const int4 d = staged || (kMode == kModeGateUp && vp.route) || kMode == kModeLinear
-                           ? pass_desc(P) : ld_const_int4(p.pass_table, P);
+                           ? pass_desc(P) : early_desc(P);
         const bool shared = kMode != kModeLinear && d.x < 0;
         const int64_t e = kMode == kModeLinear ? 0 : d.x;
         const uint8_t* wbase = shared ? p.w_shared : p.w + e * p.w_stride;
@@ -710,7 +745,7 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
         constexpr int kBlk = kK / 512;
         for (int i = wave; i < npass * 16 * kBlk; i += kVWaves) {
           const int rr = i / kBlk, bl = i - rr * kBlk;
-          const int4 d = ld_const_int4(p.pass_table, Pc + rr / 16);
+          const int4 d = early_desc(Pc + rr / 16);
           const int base = d.x < 0 ? p.T * p.top_k : d.y;
           const int row = base + min(d.w + (rr & 15), d.z - 1);
           dma16(hr, lds_a + rr * kRS + bl * 1024, static_cast<uint32_t>(lane * 16),
@@ -720,7 +755,7 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
         const buf_rsrc pr = make_rsrc(p.act_neg, static_cast<uint32_t>(hrows) * kPartRow * 4);
         for (int i = wave; i < npass * 2 * kNKB; i += kVWaves) {  // 64 partials per load, 2 kNKB per pass
           const int pass = i / (2 * kNKB), j = i - pass * 2 * kNKB;
-          const int4 d = ld_const_int4(p.pass_table, Pc + pass);
+          const int4 d = early_desc(Pc + pass);
           const int base = d.x < 0 ? p.T * p.top_k : d.y;
           const int f = 64 * j + lane, rr = f / kPartRow;
           const int row = base + min(d.w + rr, d.z - 1);
