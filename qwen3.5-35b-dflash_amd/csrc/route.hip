@@ -175,76 +175,58 @@ __device__ __forceinline__ void router_tile(const uint16_t* __restrict__ x, cons
   }
 }
 
-constexpr int kRouterAhead = 4;  // 128-column chunks of the big router tile in flight
-
-// Router logits for a 32-token x 64-expert tile (long T): the 128-column chunks
-// of both operands are staged once in LDS in MFMA fragment order (8 KB + 16 KB
-// per stage, two stages), fed from registers that keep kRouterAhead chunks in
-// flight, and each of the 8 waves computes one 16 x 16 block over the whole of
-// H = 128 kNch.  The chunk loop is straight-line code: a loop around the ring
-// makes the compiler wait for every load in flight at its head.
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // a plain vector: rings stay in registers
-struct RouterLds {
-  u32x4 sa[2][2 * 4 * 64];  // [stage][token subtile x k-step][lane]
-  u32x4 sb[2][4 * 4 * 64];  // [stage][expert subtile x k-step][lane]
-};
-
-template <int kNch>
-__device__ __forceinline__ void router_big_tile(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-                                                float* __restrict__ logits, int T, int E, int t0, int e0,
-                                                RouterLds& L) {
-  constexpr int kAhead = kRouterAhead < kNch ? kRouterAhead : kNch;
-  constexpr int H = kNch * 128;
-  auto& sa = L.sa;
-  auto& sb = L.sb;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id();
-  const int lr = lane & 15, kq = lane >> 4, tq = wave & 1, eq = wave >> 1;
-  // staging: thread copies 16-byte chunk sc of token row sr and of expert rows sr and 32 + sr
-  const int sr = tid >> 4, sc = tid & 15;
-  const u32x4* ga = reinterpret_cast<const u32x4*>(x + static_cast<int64_t>(min(t0 + sr, T - 1)) * H) + sc;
-  const u32x4* gb0 = reinterpret_cast<const u32x4*>(w + static_cast<int64_t>(min(e0 + sr, E - 1)) * H) + sc;
-  const u32x4* gb1 = reinterpret_cast<const u32x4*>(w + static_cast<int64_t>(min(e0 + 32 + sr, E - 1)) * H) + sc;
-  // fragment slot of (row r, chunk c): block (r / 16) * 4 + c / 4, lane r % 16 + 16 * (c % 4)
-  const int frag = (sc >> 2) * 64 + (sr & 15) + 16 * (sc & 3);
-  const int slot0 = (sr >> 4) * 4 * 64 + frag, slot1 = ((sr + 32) >> 4) * 4 * 64 + frag;
-  // the ring is indexed through static_for so its slots are constants (registers)
-  u32x4 ra[kAhead], rb0[kAhead], rb1[kAhead];
-  static_for(std::make_integer_sequence<int, kAhead>{}, [&](auto ic) __attribute__((always_inline)) {
-    constexpr int i = decltype(ic)::value;
-    ra[i] = ga[i * 16];
-    rb0[i] = gb0[i * 16];
-    rb1[i] = gb1[i * 16];
-  });
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  static_for(std::make_integer_sequence<int, kNch>{}, [&](auto cc) __attribute__((always_inline)) {
-    constexpr int ch = decltype(cc)::value, i = ch % kAhead;
-    constexpr int st = ch & 1;  // stage st was last read two chunks ago, before the previous barrier
-    sa[st][slot0] = ra[i];
-    sb[st][slot0] = rb0[i];
-    sb[st][slot1] = rb1[i];
-    lds_barrier();  // the later chunks' loads stay in flight
-    if constexpr (ch + kAhead < kNch) {
-      ra[i] = ga[(ch + kAhead) * 16];
-      rb0[i] = gb0[(ch + kAhead) * 16];
-      rb1[i] = gb1[(ch + kAhead) * 16];
-    }
-    u32x4 fa[4], fb[4];  // all fragments of the chunk first: one LDS wait, then the MFMA chain
+// Router logits for a 32-token x 64-expert tile (long T).  The 8 waves split H: wave w
+// takes the 32-column k-steps w, w + 8, w + 16, ... (the eight waves of a step read 512
+// contiguous bytes of every row), loads every A and B fragment of its steps straight from
+// global memory into registers, all of them in flight at once, and accumulates a partial
+// 32 x 64 tile; the partials meet in LDS and are summed in wave order.
+template <int kSteps>
+__device__ __forceinline__ void router_split_tile(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                  float* __restrict__ logits, int T, int E, int t0, int e0,
+                                                  f32x4 (*red)[8][64]) {
+  constexpr int H = kSteps * 256;
+  const int wave = threadIdx.x >> 6, lane = lane_id(), lr = lane & 15, kq = lane >> 4;
+  const uint16_t* xa[2];
+  const uint16_t* wb[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      fa[j] = sa[st][(tq * 4 + j) * 64 + lane];
-      fb[j] = sb[st][(eq * 4 + j) * 64 + lane];
-    }
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // 8 LDS reads, then 4 MFMAs
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+  for (int ts = 0; ts < 2; ++ts)
+    xa[ts] = x + static_cast<int64_t>(min(t0 + 16 * ts + lr, T - 1)) * H + wave * 32 + kq * 8;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      acc = mfma16x16x32(__builtin_bit_cast(uint4, fa[j]), __builtin_bit_cast(uint4, fb[j]), acc);
-  });
-  const int e = e0 + eq * 16 + lr;
+  for (int es = 0; es < 4; ++es)
+    wb[es] = w + static_cast<int64_t>(min(e0 + 16 * es + lr, E - 1)) * H + wave * 32 + kq * 8;
+  uint4 a[kSteps][2], b[kSteps][4];
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s) {
+#pragma unroll
+    for (int ts = 0; ts < 2; ++ts) a[s][ts] = *reinterpret_cast<const uint4*>(xa[ts] + s * 256);
+#pragma unroll
+    for (int es = 0; es < 4; ++es) b[s][es] = *reinterpret_cast<const uint4*>(wb[es] + s * 256);
+  }
+  // every load goes out before the first MFMA waits (the scheduler would otherwise sink
+  // loads between the MFMAs and wait for each soon after issuing it)
+  __builtin_amdgcn_sched_barrier(0);
+  f32x4 acc[2][4];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j >> 2][j & 3] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s)
+#pragma unroll
+    for (int ts = 0; ts < 2; ++ts)
+#pragma unroll
+      for (int es = 0; es < 4; ++es) acc[ts][es] = mfma16x16x32(a[s][ts], b[s][es], acc[ts][es]);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) red[wave][j][lane] = acc[j >> 2][j & 3];
+  __syncthreads();
+  // thread (j, lane) sums block j = (token subtile, expert subtile) of the eight partials
+  const int j = wave;
+  f32x4 sum = red[0][j][lane];
+#pragma unroll
+  for (int v = 1; v < 8; ++v) sum += red[v][j][lane];
+  const int e = e0 + 16 * (j & 3) + lr;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int t = t0 + tq * 16 + 4 * kq + i;
-    if (t < T && e < E) logits[static_cast<int64_t>(t) * E + e] = acc[i];
+    const int t = t0 + 16 * (j >> 2) + 4 * kq + i;
+    if (t < T && e < E) logits[static_cast<int64_t>(t) * E + e] = sum[i];
   }
 }
 
@@ -272,12 +254,17 @@ __global__ __launch_bounds__(512) void front_kernel(FrontParams p) {
   }
   b -= p.n_zero;
   if (p.router_big) {
-    __shared__ RouterLds lds;  // one buffer for every H instance
-    const int tiles_e = (p.E + 63) / 64;
-    const int t0 = (b / tiles_e) * 32, e0 = (b % tiles_e) * 64;
-    if (p.H == 512) router_big_tile<4>(p.x, p.router_w, p.logits, p.T, p.E, t0, e0, lds);
-    else if (p.H == 1024) router_big_tile<8>(p.x, p.router_w, p.logits, p.T, p.E, t0, e0, lds);
-    else router_big_tile<16>(p.x, p.router_w, p.logits, p.T, p.E, t0, e0, lds);
+    __shared__ f32x4 red[8][8][64];  // one buffer for every H instance
+    // the expert tiles of a token tile share its rows: blocks b, b + 8, ... of a group of
+    // 8 token tiles take them (consecutive workgroups go to different XCDs, each with its L2)
+    const int tiles_e = (p.E + 63) / 64, tiles_t = (p.T + 31) / 32;
+    const int group = b / (8 * tiles_e), r = b - group * 8 * tiles_e;
+    const bool whole = group * 8 + 8 <= tiles_t;
+    const int tt = group * 8 + (whole ? r % 8 : r / tiles_e), te = whole ? r / 8 : r % tiles_e;
+    const int t0 = tt * 32, e0 = te * 64;
+    if (p.H == 512) router_split_tile<2>(p.x, p.router_w, p.logits, p.T, p.E, t0, e0, red);
+    else if (p.H == 1024) router_split_tile<4>(p.x, p.router_w, p.logits, p.T, p.E, t0, e0, red);
+    else router_split_tile<8>(p.x, p.router_w, p.logits, p.T, p.E, t0, e0, red);
   } else {
     const int tiles_e = (p.E + 15) / 16;
     router_tile(p.x, p.router_w, p.logits, p.T, p.E, p.H, (b / tiles_e) * 16, (b % tiles_e) * 16);

@@ -164,3 +164,21 @@ def test_measure_stage_relaunches_one_kernel(pkg, device):
         assert torch.equal(ws, snapshot), stage
     again = pkg.ops.moe_w4a16(x, gu, dn, top_k=8, router_weight=rw, shared=sh, workspace=ws)
     assert torch.equal(again, ref)
+
+
+def test_empty_batch(pkg, device):
+    """Zero tokens: empty outputs and the oracle's all-zero expert offsets from every entry point."""
+    from oracle import routing
+    layer = pkg.synthetic.moe_layer(4, hidden=512, inter=512, experts=8, seed=2)
+    gu, dn, sh = _to(pkg, layer, device)
+    _, _, offsets = routing.permutation(np.zeros((0, 2), np.int32), 8)
+    x = torch.empty((0, 512), dtype=torch.bfloat16, device=device)
+    out, r, logits = pkg.ops.moe_w4a16(x, gu, dn, top_k=2, router_weight=layer.router_weight.to(device), shared=sh,
+                                       return_routing=True)
+    assert tuple(out.shape) == (0, 512) and tuple(r.ids.shape) == (0, 2) and tuple(logits.shape) == (0, 8)
+    np.testing.assert_array_equal(r.offsets.cpu().numpy(), offsets)
+    r2 = pkg.ops.route(torch.empty((0, 8), dtype=torch.float32, device=device), 2)
+    np.testing.assert_array_equal(r2.offsets.cpu().numpy(), offsets)
+    assert tuple(pkg.ops.moe_experts(x, r2, gu, dn, shared=sh).shape) == (0, 512)
+    w = pkg.packing.quantize_w4(torch.randn((64, 512)).to(torch.bfloat16), 128).to(device)
+    assert tuple(pkg.ops.qlinear(x, w).shape) == (0, 64)

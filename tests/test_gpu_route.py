@@ -88,9 +88,14 @@ def test_router_logits(pkg, device, tokens):
     assert report["max_rel"] <= 1e-5, report
 
 
-@pytest.mark.parametrize("tokens,experts,hidden", [(100, 100, 1024), (65, 200, 768)])
+@pytest.mark.parametrize("tokens,experts,hidden", [
+    (100, 100, 1024), (65, 200, 768),
+    (300, 200, 512),      # 10 token tiles: one whole group of 8 and a partial group of 2
+    (64, 64, 2048),       # one partial group, one expert tile
+    (1000, 256, 1024),    # 32 token tiles, four whole groups, ragged last token tile
+])
 def test_router_logits_ragged_tiles(pkg, device, tokens, experts, hidden):
-    """Token and expert counts that leave partial 32 x 64 router tiles."""
+    """Token and expert counts that leave partial 32 x 64 router tiles and partial tile groups."""
     print(f"router T={tokens} E={experts} H={hidden}", flush=True)
     gen = torch.Generator().manual_seed(tokens + experts)
     x = torch.randn((tokens, hidden), generator=gen).to(torch.bfloat16)
