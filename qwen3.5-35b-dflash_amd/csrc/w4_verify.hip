@@ -348,7 +348,14 @@ __device__ int route_rows(const VerifyParams& vp, RowKeys<kPR> keys, char* lds, 
         if (tp < npass) {
           const uint32_t rm = half_reduce<false>(keys_max<kPR>(keys.key[tp]));
           const uint32_t first = keys_first<kPR>(keys.key[tp], rm);
-          const uint32_t e = half_reduce<true>(first < kPR ? static_cast<uint32_t>(kPR * r) + first : 0xFFFFu);
+          // expert ids grow with the lane, so the lowest lane of the half-wave that holds rm
+          // holds the lowest id among the equal keys (every half-wave has one: rm is its max)
+          const uint64_t holds = __ballot(first < kPR);
+          const int l0 = __builtin_ctz(static_cast<uint32_t>(holds));
+          const int l1 = 32 + __builtin_ctz(static_cast<uint32_t>(holds >> 32));
+          const uint32_t e0 = static_cast<uint32_t>(kPR * l0) + __builtin_amdgcn_readlane(first, l0);
+          const uint32_t e1 = static_cast<uint32_t>(kPR * (l1 - 32)) + __builtin_amdgcn_readlane(first, l1);
+          const uint32_t e = (threadIdx.x & 32) ? e1 : e0;
           const uint32_t ie = e - static_cast<uint32_t>(kPR * r);  // wraps past kPR unless this lane's
 #pragma unroll
           for (int i = 0; i < kPR; ++i) keys.key[tp][i] = ie == static_cast<uint32_t>(i) ? 0u : keys.key[tp][i];

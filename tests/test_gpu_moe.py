@@ -182,3 +182,24 @@ def test_empty_batch(pkg, device):
     assert tuple(pkg.ops.moe_experts(x, r2, gu, dn, shared=sh).shape) == (0, 512)
     w = pkg.packing.quantize_w4(torch.randn((64, 512)).to(torch.bfloat16), 128).to(device)
     assert tuple(pkg.ops.qlinear(x, w).shape) == (0, 64)
+
+
+@pytest.mark.parametrize("tokens,experts,k", [(16, 256, 8), (32, 64, 8), (7, 128, 4)])
+def test_moe_in_kernel_routing_ties(pkg, device, tokens, experts, k):
+    """Logits on a coarse grid (many equal values per token, -0.0 and +0.0 among them): the
+    routing inside the gate/up launch must break ties by the lowest expert id, as the oracle does."""
+    print(f"moe ties T={tokens} E={experts} k={k}", flush=True)
+    layer = pkg.synthetic.moe_layer(tokens, hidden=2048, inter=512, experts=experts, seed=40 + tokens)
+    gen = torch.Generator().manual_seed(tokens * 7 + experts)
+    lg = torch.round(torch.randn((tokens, experts), generator=gen) * 1.5) / 2
+    lg[lg == 0] = torch.where(torch.rand(int((lg == 0).sum()), generator=gen) < 0.5, -0.0, 0.0)
+    gu, dn, sh = _to(pkg, layer, device)
+    out, r, _ = pkg.ops.moe_w4a16(layer.hidden.to(device), gu, dn, top_k=k, router_logits=lg.to(device), shared=sh,
+                                  return_routing=True)
+    ogu, odn, osh = _oracle_banks(layer)
+    golden = oracle_moe.moe(layer.hidden, lg.numpy(), k, ogu, odn, layer.gate_up.group_size, shared=osh)
+    np.testing.assert_array_equal(r.ids.cpu().numpy(), golden["ids"])
+    np.testing.assert_array_equal(r.perm.cpu().numpy(), golden["perm"])
+    np.testing.assert_array_equal(r.offsets.cpu().numpy(), golden["offsets"])
+    np.testing.assert_allclose(r.weights.cpu().numpy(), golden["weights"], rtol=0, atol=2e-6)
+    assert metrics.compare(out.cpu(), golden["out_f32"])["max_rel"] <= TOL
