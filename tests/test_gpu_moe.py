@@ -97,6 +97,10 @@ def test_moe_prefill_t2048(pkg, device):
     (16, 256, 8, 2048, 512, 256, torch.float32, True),        # verify kernels, the reference quantizer's g256 fp32
     (5, 8, 2, 512, 512, 256, torch.bfloat16, False),          # verify kernels, group 256, K = 512 (one group per 2 k-blocks)
     (32, 64, 8, 2048, 1024, 256, torch.float32, True),        # verify kernels at their largest T, group 256
+    (16, 200, 8, 512, 512, 128, torch.bfloat16, True),        # half-wave routing, 8 keys a lane, E not a multiple of 32
+    (16, 512, 8, 512, 512, 128, torch.bfloat16, True),        # verify kernels, block routing (E > 256)
+    (24, 1024, 4, 512, 512, 128, torch.float32, False),       # block routing at the largest expert count
+    (32, 300, 8, 512, 512, 256, torch.bfloat16, True),        # block routing, two token passes, group 256
 ])
 def test_moe_small_shapes(pkg, device, tokens, experts, k, hidden, inter, group, scale_dtype, shared):
     print(f"moe T={tokens} E={experts} k={k} H={hidden} I={inter} g={group} {scale_dtype} shared={shared}",
