@@ -440,9 +440,13 @@ __global__ __launch_bounds__(256) void route_permute_kernel(RouteParams p) {
   const int c0 = lane * per_lane, c1 = min(c0 + per_lane, pitch >> 4);
   const uint4 zero4 = make_uint4(0u, 0u, 0u, 0u);
   const uint4 r0 = c0 < c1 ? row[c0] : zero4, r1 = c0 + 1 < c1 ? row[c0 + 1] : zero4;
+  // the counts of the experts below e: every load in flight at once (a rolled loop waits for
+  // each before issuing the next); the resource reads 0 from e on
   int before = 0, nz_before = 0, pass_before = 0;
-  for (int i = lane; i < e; i += 64) {
-    const int c = p.counts[i];
+  const buf_rsrc cr = make_rsrc(p.counts, static_cast<uint32_t>(e) * 4);
+#pragma unroll
+  for (int j = 0; j < kMaxExperts / 64; ++j) {
+    const int c = static_cast<int>(__float_as_uint(buf_load_f32(cr, static_cast<uint32_t>(lane + 64 * j) * 4, 0)));
     before += c;
     nz_before += c > 0 ? 1 : 0;
     pass_before += passes_for(c, p.rows_per_pass);
@@ -478,9 +482,20 @@ __global__ __launch_bounds__(256) void route_permute_kernel(RouteParams p) {
   int mine = nonzero_bytes(r0) + nonzero_bytes(r1);
   for (int c = c0 + 2; c < c1; ++c) mine += nonzero_bytes(row[c]);
   int pos = before + wave_exclusive_scan(mine);
+  // the routing weights of a chunk's pairs come in one batch of loads ahead of the writes
+  // (a load inside each pair's branch would wait once per byte position); empty bytes load
+  // past the end of the resource, which reads 0 without touching memory
+  const buf_rsrc wr = make_rsrc(p.wts, static_cast<uint32_t>(p.T * p.k) * 4);
   for (int c = c0; c < c1 && mine > 0; ++c) {
     const uint4 v = c == c0 ? r0 : c == c0 + 1 ? r1 : row[c];
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    float wt[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int slot1 = (w[q >> 2] >> (8 * (q & 3))) & 0xFF;
+      const uint32_t off = slot1 ? static_cast<uint32_t>(((16 * c + q) * p.k + slot1 - 1) * 4) : 0xFFFFFFF0u;
+      wt[q] = buf_load_f32(wr, off, 0);
+    }
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
       const int slot1 = (w[q >> 2] >> (8 * (q & 3))) & 0xFF;
@@ -489,7 +504,7 @@ __global__ __launch_bounds__(256) void route_permute_kernel(RouteParams p) {
         const int flat = t * p.k + slot1 - 1;
         p.perm[pos] = flat;
         p.inv[flat] = pos;
-        p.slot_w[pos] = p.wts[flat];
+        p.slot_w[pos] = wt[q];
         p.tok[pos] = t;
         ++pos;
         --mine;
