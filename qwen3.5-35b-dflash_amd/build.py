@@ -15,7 +15,7 @@ from pathlib import Path
 
 PACKAGE_DIR = Path(__file__).resolve().parent
 LIBRARY = PACKAGE_DIR / "libdflash_hip.so"
-SOURCES = ("csrc/api.hip", "csrc/route.hip", "csrc/w4_gemm.hip", "csrc/w4_stream.hip", "csrc/w4_wave.hip",
+SOURCES = ("csrc/api.hip", "csrc/route.hip", "csrc/w4_gemm.hip", "csrc/w4_stream.hip",
            "csrc/w4_tile.hip", "csrc/w4_verify.hip",
            "csrc/repack.hip")
 ARCH = "gfx950"

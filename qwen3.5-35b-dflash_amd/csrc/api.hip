@@ -62,7 +62,7 @@ int check_w4(const dflash_w4* w, const char* name, int64_t experts, int64_t rows
   return DFLASH_OK;
 }
 
-// The wave-streaming and per-wave fallback kernels read portable rows only.
+// The per-wave fallback kernel (w4_gemm) reads portable rows only.
 int tiled_unsupported(const char* what) {
   return fail(DFLASH_ERR_UNSUPPORTED, std::string(what) +
                                           ": tiled weights are streamed by the verify, streaming and tile kernels "
@@ -139,9 +139,10 @@ int cu_count() {
 
 int token_tiles(int64_t T) { return T <= 16 ? 1 : 2; }
 
-// Small token counts run both expert GEMMs on the wave-streaming kernel, whose
-// passes hold 16 rows; larger T uses passes of 16 * token_tiles(T) rows.
-constexpr int64_t kWaveMaxTokens = 32;
+// The verify kernels take blocks of at most 32 tokens and 2048 routed slot rows;
+// other small blocks use passes of 16 * token_tiles(T) rows on the streaming kernel.
+constexpr int64_t kVerifyMaxTokens = 32;
+constexpr int64_t kVerifyMaxTokenRows = 2048;
 
 int check_route_args(int64_t T, int64_t E, int64_t k) {
   if (T < 0) return fail(DFLASH_ERR_INVALID_ARGUMENT, "tokens must be >= 0");
@@ -149,6 +150,8 @@ int check_route_args(int64_t T, int64_t E, int64_t k) {
   if (E <= 0 || E > dflash::kMaxExperts) return fail(DFLASH_ERR_UNSUPPORTED, "experts must be in [1, 1024]");
   if (k <= 0 || k > E || k > dflash::kMaxTopK)
     return fail(DFLASH_ERR_INVALID_ARGUMENT, "top_k must be in (0, min(experts, 64)]");
+  // routing offsets and buffer sizes (T*k*4 bytes, byte offsets of (T*k + T) rows) stay in 32 bits
+  if (T * k > (int64_t(1) << 28)) return fail(DFLASH_ERR_UNSUPPORTED, "tokens * top_k above 2^28 is not supported");
   return DFLASH_OK;
 }
 
@@ -160,30 +163,23 @@ struct MoeShapes {
   bool tiled;     // every bank in the tiled layout
 };
 
-bool moe_wave_path(const MoeShapes& S) {
-  using namespace dflash;
-  return S.T <= kWaveMaxTokens && S.T * S.k <= kWaveMaxTokenRows && S.G == 128 && S.Gd == 128 && S.scales16 &&
-         w4_wave_supports(kModeGateUp, static_cast<int>(S.H), 128, static_cast<int>(S.T)) &&
-         w4_wave_supports(kModeDown, static_cast<int>(S.I), 128, 0);
-}
-
 // Long prefill (at least 16 rows per expert on average) runs both expert GEMMs
 // on the LDS-tiled kernel, whose passes hold 96 rows.
 bool moe_tile_path(const MoeShapes& S) {
   using namespace dflash;
   const int64_t rows = S.T * S.k + S.T;
-  return !moe_wave_path(S) && S.T * S.k >= 16 * S.E && rows * std::max(S.H, S.I) < (int64_t(1) << 31) &&
+  return S.T * S.k >= 16 * S.E && rows * std::max(S.H, S.I) < (int64_t(1) << 31) &&
          w4_tile_supports(kModeGateUp, static_cast<int>(2 * S.I), static_cast<int>(S.H), static_cast<int>(S.G)) &&
          w4_tile_supports(kModeDown, static_cast<int>(S.H), static_cast<int>(S.I), static_cast<int>(S.Gd));
 }
 
 bool verify_fits(const MoeShapes& S, bool route, dflash::VerifyParams* gu, dflash::VerifyParams* dn);
 
-// Rows per pass of the work table: 16 on the verify and wave paths (T <= 32), 96 on
+// Rows per pass of the work table: 16 on the verify path (T <= 32), 96 on
 // the prefill tile path, else 16 per token tile of the streaming kernel.
 int rows_per_pass(const MoeShapes& S) {
   dflash::VerifyParams gu, dn;
-  if (verify_fits(S, false, &gu, &dn) || moe_wave_path(S)) return 16;
+  if (verify_fits(S, false, &gu, &dn)) return 16;
   if (moe_tile_path(S)) return dflash::kTileRowsPerPass;
   return 16 * token_tiles(S.T);
 }
@@ -234,10 +230,10 @@ bool stage_on(int stage) {
   return m == DFLASH_STAGE_NONE || m == stage;
 }
 
-// One W4 GEMM over the work table: the wave-streaming kernel for small T
-// (wave == true), else the workgroup-streaming kernel when it splits this K
-// evenly, else the per-wave fallback.
-enum class GemmPath { kWave, kTile, kStream };
+// One W4 GEMM over the work table: the LDS-tiled kernel for long prefill, else
+// the workgroup-streaming kernel when it splits this K evenly, else the per-wave
+// fallback (w4_gemm: K outside {512, 1024, 2048} or group 256).
+enum class GemmPath { kTile, kStream };
 
 void launch_w4(int mode, bool fp32_scales, int mt, int max_slots, GemmPath path, dflash::W4StreamParams& p,
                hipStream_t stream) {
@@ -248,11 +244,6 @@ void launch_w4(int mode, bool fp32_scales, int mt, int max_slots, GemmPath path,
     return;
   }
   const int cols = mode == kModeGateUp ? p.N / 2 / 16 : p.N / 32;  // 16-column pairs or 32-row strips
-  if (path == GemmPath::kWave) {
-    p.strips = cols;
-    launch_w4_wave(mode, fp32_scales, cu_count(), p, stream);
-    return;
-  }
   const int rg = w4_stream_row_groups(p.K);
   if (w4_stream_supports(p.K, p.G) && cols % rg == 0) {
     p.strips = cols / rg;
@@ -263,11 +254,10 @@ void launch_w4(int mode, bool fp32_scales, int mt, int max_slots, GemmPath path,
 }
 
 // Whether launch_w4 would run a kernel that reads the tiled layout (tile, or the
-// streaming kernel when it splits this K); the wave and per-wave fallbacks do not.
+// streaming kernel when it splits this K); the per-wave fallback does not.
 bool w4_path_reads_tiled(int mode, int N, int K, int G, GemmPath path) {
   using namespace dflash;
   if (path == GemmPath::kTile) return true;
-  if (path == GemmPath::kWave) return false;
   const int cols = mode == kModeGateUp ? N / 2 / 16 : N / 32;
   return w4_stream_supports(K, G) && cols % w4_stream_row_groups(K) == 0;
 }
@@ -278,7 +268,7 @@ bool w4_path_reads_tiled(int mode, int N, int K, int G, GemmPath path) {
 bool verify_fits(const MoeShapes& S, bool route, dflash::VerifyParams* gu, dflash::VerifyParams* dn) {
   using namespace dflash;
   const auto group_ok = [](int64_t g) { return g == 128 || g == 256; };
-  if (S.T > kWaveMaxTokens || S.T * S.k > kWaveMaxTokenRows || !group_ok(S.G) || !group_ok(S.Gd)) return false;
+  if (S.T > kVerifyMaxTokens || S.T * S.k > kVerifyMaxTokenRows || !group_ok(S.G) || !group_ok(S.Gd)) return false;
   const int T = static_cast<int>(S.T), H = static_cast<int>(S.H), I = static_cast<int>(S.I);
   const int E = static_cast<int>(S.E), k = static_cast<int>(S.k), sh = S.shared ? 1 : 0;
   *gu = VerifyParams{};
@@ -394,7 +384,7 @@ int run_verify(const MoeShapes& S, dflash::VerifyParams gu, dflash::VerifyParams
 // Every kernel input besides x and the weight banks comes from the workspace
 // (routing kernels or table_prep wrote it); inv (the caller's) feeds combine.
 GemmPath moe_gemm_path(const MoeShapes& S) {
-  return moe_wave_path(S) ? GemmPath::kWave : moe_tile_path(S) ? GemmPath::kTile : GemmPath::kStream;
+  return moe_tile_path(S) ? GemmPath::kTile : GemmPath::kStream;
 }
 
 // Tiled banks need every expert kernel of the call to read that layout; checked
@@ -601,16 +591,14 @@ int dflash_qlinear_w4a16(const void* x, int64_t m, const dflash_w4* weight, void
     if (!workspace || workspace_bytes < need || !aligned16(workspace))
       return fail(DFLASH_ERR_WORKSPACE, "qlinear workspace needs " + std::to_string(need) + " bytes");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    // GEMM kernel: verify (m <= 32, group 128), else wave-streaming for portable weights
-    // that fit, else the streaming kernel (or its per-wave fallback)
+    // GEMM kernel: verify (m <= 32), else the streaming kernel (or its per-wave fallback)
     const bool tiled = weight->layout == DFLASH_LAYOUT_TILED;
     dflash::VerifyParams vl{};
+    // the verify kernel stages at most 16 rows of K = 4096; 17..32 rows run as two launches of it
+    const int64_t vrows = K == 4096 && m > 16 && m <= 32 ? 16 : m;
     const bool verify = (weight->group_size == 128 || weight->group_size == 256) &&
-                        dflash::verify_layout(dflash::kModeLinear, static_cast<int>(m), static_cast<int>(K),
+                        dflash::verify_layout(dflash::kModeLinear, static_cast<int>(vrows), static_cast<int>(K),
                                               static_cast<int>(N), 1, 1, 0, 0, &vl);
-    const bool wave = !verify && !tiled && aligned16(weight->scales) &&
-                      dflash::w4_wave_supports(dflash::kModeLinear, static_cast<int>(K),
-                                               static_cast<int>(weight->group_size), static_cast<int>(m));
     if (tiled && !verify &&
         !w4_path_reads_tiled(dflash::kModeLinear, static_cast<int>(N), static_cast<int>(K),
                              static_cast<int>(weight->group_size), GemmPath::kStream))
@@ -642,17 +630,22 @@ int dflash_qlinear_w4a16(const void* x, int64_t m, const dflash_w4* weight, void
     p.out_bf16 = static_cast<uint16_t*>(y);
     p.M = static_cast<int>(m);
     if (verify) {
-      p.act = static_cast<const uint16_t*>(x);
       p.act_neg = nullptr;
       p.rows_per_pass = 16;
       p.strips = p.N / 32;
-      vl.g = p;
-      dflash::launch_w4_verify(dflash::kModeLinear, weight->scale_dtype == DFLASH_DTYPE_F32, cu_count(), vl, st);
-      return launch_status("qlinear");
+      for (int64_t r0 = 0; r0 < m; r0 += vrows) {
+        p.act = static_cast<const uint16_t*>(x) + r0 * K;
+        p.out_bf16 = static_cast<uint16_t*>(y) + r0 * N;
+        p.M = static_cast<int>(std::min(vrows, m - r0));
+        vl.g = p;
+        dflash::launch_w4_verify(dflash::kModeLinear, weight->scale_dtype == DFLASH_DTYPE_F32, cu_count(), vl, st);
+        if (int r = launch_status("qlinear")) return r;
+      }
+      return DFLASH_OK;
     }
-    const int mt = wave ? 1 : token_tiles(m);
+    const int mt = token_tiles(m);
     p.rows_per_pass = 16 * mt;
-    launch_w4(dflash::kModeLinear, weight->scale_dtype == DFLASH_DTYPE_F32, mt, 1, wave ? GemmPath::kWave : GemmPath::kStream,
+    launch_w4(dflash::kModeLinear, weight->scale_dtype == DFLASH_DTYPE_F32, mt, 1, GemmPath::kStream,
               p, st);
     return launch_status("qlinear");
   } catch (...) {

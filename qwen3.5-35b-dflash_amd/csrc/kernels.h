@@ -161,11 +161,6 @@ bool w4_stream_supports(int K, int G);
 int w4_stream_row_groups(int K);
 // mt: token tiles per pass (1 or 2); grid: persistent workgroups (one per CU)
 void launch_w4_stream(int mode, bool fp32_scales, int mt, int grid, const W4StreamParams& p, hipStream_t stream);
-// Wave-streaming kernel for small T (w4_wave.hip): 16-row passes, group 128, K in {512, 1024, 2048}.
-// rows: activation rows kept in LDS (T for gate_up, M for linear; ignored for down).
-bool w4_wave_supports(int mode, int K, int G, int rows);
-constexpr int kWaveMaxTokenRows = 2048;  // T * top_k routed slot rows whose tokens stay in LDS
-void launch_w4_wave(int mode, bool fp32_scales, int grid, const W4StreamParams& p, hipStream_t stream);
 // Verify-block expert kernels (w4_verify.hip), T <= 32 tokens: 16-row passes,
 // group 128, K in {512, 1024, 2048}.  Each workgroup splits its contiguous
 // range of units evenly over its 8 waves at k-block granularity; units split
@@ -199,7 +194,7 @@ struct VerifyParams {
   int down_grid, down_strips;
 };
 // LDS bytes and layout of one verify launch; false when it does not fit (the
-// caller keeps the separate routing / wave-streaming kernels then).
+// caller keeps the separate routing / streaming kernels then).
 bool verify_layout(int mode, int T, int K, int N, int E, int k, int has_shared, int route, VerifyParams* vp);
 void launch_w4_verify(int mode, bool fp32_scales, int grid, const VerifyParams& vp, hipStream_t stream);
 // LDS-tiled kernel for long prefill (w4_tile.hip): 96-row passes, column tiles of 512

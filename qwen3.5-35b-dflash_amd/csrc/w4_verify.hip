@@ -950,6 +950,8 @@ bool verify_layout(int mode, int T, int K, int N, int E, int k, int has_shared, 
   L.lds_neg = take(((T * nkb + 63) & ~63) * 4);  // filled 64 terms per direct-to-LDS load
   L.lds_wgt = 0;
   if (mode == kModeLinear) {
+    // stage_x_raw gives each thread at most 16 chunks of 8 columns: 32 rows up to K = 2048, 16 at K = 4096
+    if (T * (K / 8) > kVThreads * std::min(nkb, 16)) return false;
     L.pd_cap = 0;
     L.lds_tok = L.lds_pdesc = 0;
     L.lds_part = L.lds_scratch = take(part);

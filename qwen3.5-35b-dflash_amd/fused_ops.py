@@ -4,9 +4,9 @@ Drop-in for the reference's operator seam: a module with ``FUSED_OPS_ABI = 1``,
 a ``BACKEND_ID`` and the seven callables that
 ``model/qwen35_moe_dflash/fused/ops.py:126-176`` (``ModuleFusedOps``) binds.
 ``moe`` and ``qlinear`` run on the hand-written HIP kernels of
-``libdflash_hip.so``; the six non-hot operations are plain PyTorch
-restatements of ``reference/fused_ops.py:28-145`` that run on whatever device
-their inputs are on.
+``libdflash_hip.so``; the six non-hot operations are batched PyTorch code of
+this backend's own that runs on whatever device its inputs are on (the
+protocol they satisfy is ``fused/ops.py:25-123``).
 
 Physical format (the explicit adapter contract that
 ``fused/ops.py:117-122`` asks packed weights to have): ``gate_up`` and
@@ -21,7 +21,6 @@ import math
 from typing import Optional
 
 import torch
-import torch.nn.functional as F
 from torch import Tensor
 
 from . import ops
@@ -33,111 +32,180 @@ IS_REFERENCE_BACKEND = False
 
 
 # ------------------------------------------------------------------ non-hot ops
+# The contract of each op (signature, shapes, dtypes and the ValueError messages a caller
+# may match on) is the FusedOps protocol of ``fused/ops.py:25-123``; the bodies are this
+# backend's own: batched tensor algebra that runs on the inputs' device in a handful of
+# launches (no per-token Python loop, no materialised GQA repeat of the KV cache).
+
+def _require(ok: bool, message: str) -> None:
+    if not ok:
+        raise ValueError(message)
+
+
+def _is_int(v) -> bool:
+    return isinstance(v, int) and not isinstance(v, bool)
+
+
 def rms_norm(x: Tensor, gamma: Tensor, eps: float) -> Tensor:
-    """``x * rsqrt(mean(x^2) + eps)`` in fp32, cast back, times the given (effective) gamma."""
-    if not math.isfinite(eps) or eps <= 0 or tuple(gamma.shape) != tuple(x.shape[-1:]):
-        raise ValueError("RMSNorm needs positive epsilon and one gamma per feature")
+    """``x / rms(x)`` computed in fp32 and rounded to ``x.dtype``, then times the effective gamma.
+
+    The gamma given is the effective one (the caller adds any +1 offset).
+    """
+    _require(tuple(gamma.shape) == tuple(x.shape[-1:]) and math.isfinite(eps) and eps > 0,
+             "RMSNorm needs positive epsilon and one gamma per feature")
     xf = x.float()
-    scale = torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + eps)
-    return (xf * scale).to(x.dtype) * gamma
+    mean_square = torch.linalg.vector_norm(xf, dim=-1, keepdim=True).square_().div_(x.shape[-1])
+    return (xf * mean_square.add_(eps).rsqrt_()).to(x.dtype) * gamma
 
 
 def conv_state_update(projected: Tensor, history: Tensor) -> tuple[Tensor, Tensor]:
-    """``[B,S,C]`` + history ``[B,C,K-1]`` -> (new history ``[B,C,K-1]``, padded ``[B,C,S+K-1]``)."""
-    if (projected.ndim != 3 or history.ndim != 3 or projected.shape[1] < 1
-            or projected.shape[0] != history.shape[0] or projected.shape[2] != history.shape[1]
-            or projected.dtype != history.dtype):
-        raise ValueError("conv state requires projected [B,S,C] and matching history [B,C,K-1]")
-    padded = torch.cat([history, projected.permute(0, 2, 1)], dim=2)
+    """``[B,S,C]`` + history ``[B,C,K-1]`` -> (new history ``[B,C,K-1]``, window ``[B,C,K-1+S]``).
+
+    The window is the history followed by the new columns; the new history is its
+    last ``K-1`` columns, returned as a tensor of its own.
+    """
+    _require(projected.ndim == 3 and history.ndim == 3 and projected.shape[1] >= 1
+             and (projected.shape[0], projected.shape[2]) == tuple(history.shape[:2])
+             and projected.dtype == history.dtype,
+             "conv state requires projected [B,S,C] and matching history [B,C,K-1]")
     keep = history.shape[2]
-    new_history = padded[:, :, padded.shape[2] - keep:].clone() if keep else padded[:, :, :0].clone()
-    return new_history, padded
+    window = projected.new_empty((projected.shape[0], projected.shape[2], keep + projected.shape[1]))
+    window[:, :, :keep] = history
+    window[:, :, keep:] = projected.transpose(1, 2)
+    return window[:, :, window.shape[2] - keep:].clone(), window
 
 
 def causal_conv1d(padded: Tensor, weight: Tensor) -> Tensor:
-    """Depthwise causal conv ``[B,C,S+K-1]`` x ``[C,1,K]`` -> ``[B,S,C]`` (no activation)."""
-    if (padded.ndim != 3 or weight.ndim != 3 or weight.shape[1] != 1
-            or padded.shape[1] != weight.shape[0] or weight.shape[2] < 1
-            or padded.shape[2] < weight.shape[2] or padded.dtype != weight.dtype):
-        raise ValueError("depthwise conv requires [B,C,S+K-1] and [C,1,K]")
-    out = F.conv1d(padded, weight, groups=weight.shape[0])
-    return out.permute(0, 2, 1).contiguous()
+    """Depthwise causal conv ``[B,C,K-1+S]`` with taps ``[C,1,K]`` -> ``[B,S,C]`` (no activation).
+
+    Output column ``s`` of channel ``c`` is ``sum_j weight[c,0,j] * padded[c, s+j]``: the
+    ``K`` taps are read as one strided window view and reduced in a single pass.
+    """
+    _require(padded.ndim == 3 and weight.ndim == 3 and weight.shape[1] == 1 and weight.shape[2] >= 1
+             and padded.shape[1] == weight.shape[0] and padded.shape[2] >= weight.shape[2]
+             and padded.dtype == weight.dtype,
+             "depthwise conv requires [B,C,S+K-1] and [C,1,K]")
+    taps = weight.shape[2]
+    windows = padded.unfold(2, taps, 1)                      # [B, C, S, K] view, no copy
+    out = (windows.float() * weight[:, 0, None, :].float()).sum(-1)
+    return out.to(padded.dtype).transpose(1, 2).contiguous()
+
+
+def _delta_rule_chunk(q, k, v, g, beta, state):
+    """One chunk of the gated delta rule in closed (WY) form, fp32, batched over [B, H].
+
+    With ``G_t = sum_{s<=t} g_s`` the recurrence ``S_t = e^{g_t} S_{t-1} + k_t u_t^T``,
+    ``u_t = beta_t (v_t - e^{g_t} S_{t-1}^T k_t)`` unrolls to the unit lower-triangular
+    system ``(I + A) U = diag(beta) (V - diag(e^G) K S_0)`` with
+    ``A_ts = beta_t e^{G_t - G_s} k_t.k_s`` (s < t); then
+    ``o_t = e^{G_t} S_0^T q_t + sum_{s<=t} e^{G_t - G_s} (q_t.k_s) u_s`` and
+    ``S_C = e^{G_C} S_0 + sum_s e^{G_C - G_s} k_s u_s^T``.  Every decay factor used is
+    ``e^{G_t - G_s}`` with ``s <= t`` (at most 1): no overflow for long chunks.
+    Shapes: q, k ``[B,H,C,Dk]``, v ``[B,H,C,Dv]``, g, beta ``[B,H,C]``, state ``[B,H,Dk,Dv]``.
+    """
+    c = q.shape[2]
+    cum = torch.cumsum(g, dim=-1)                                   # G_t
+    diff = cum[..., :, None] - cum[..., None, :]                    # G_t - G_s
+    causal = torch.ones((c, c), dtype=torch.bool, device=q.device).tril()
+    decay = torch.where(causal, diff, torch.full_like(diff, -math.inf)).exp()   # 0 above the diagonal
+    strict = (decay * (k @ k.transpose(-1, -2)) * beta[..., :, None]).tril(-1)
+    head = cum.exp()[..., None]                                     # e^{G_t}
+    rhs = beta[..., None] * (v - head * (k @ state))
+    eye = torch.eye(c, dtype=q.dtype, device=q.device)
+    u = torch.linalg.solve_triangular(eye + strict, rhs, upper=False, unitriangular=True)
+    out = head * (q @ state) + (decay * (q @ k.transpose(-1, -2))) @ u
+    tail = (cum[..., -1:] - cum).exp()[..., None]                   # e^{G_C - G_s}
+    new_state = cum[..., -1:, None].exp() * state + (k * tail).transpose(-1, -2) @ u
+    return out, new_state
 
 
 def chunk_gated_delta_rule(query: Tensor, key: Tensor, value: Tensor, g: Tensor, beta: Tensor,
                            initial_state: Tensor, effective_length: Tensor, *, chunk_size: int,
                            use_qk_l2norm_in_kernel: bool) -> tuple[Tensor, Tensor]:
-    """Gated delta rule, token by token; only the first ``effective_length`` tokens update state."""
-    if isinstance(chunk_size, bool) or chunk_size not in (1, 64):
-        raise ValueError("chunk_size must be 1 or 64")
-    if not isinstance(use_qk_l2norm_in_kernel, bool):
-        raise ValueError("use_qk_l2norm_in_kernel must be bool")
-    if (query.ndim != 4 or key.shape != query.shape or value.ndim != 4
-            or value.shape[:3] != query.shape[:3] or g.shape != query.shape[:3]
-            or beta.shape != query.shape[:3] or min(query.shape) < 1 or value.shape[-1] < 1):
-        raise ValueError("GDN requires compatible [B,S,H,D] tensors and [B,S,H] gates")
+    """Gated delta rule over ``[B,S,H,D]`` tokens; returns core ``[B,S,H,Dv]`` and the final state.
+
+    Tokens at or past ``effective_length[b]`` leave the state unchanged and output zeros
+    (they enter the chunk with ``g = 0`` and ``beta = 0``).  Math in fp32, chunks of 64
+    tokens (``chunk_size`` is the caller's decode/prefill tag, 1 or 64; the closed chunk
+    form is exact for any length).  Q/K are L2-normalised here when asked to be
+    (``q / sqrt(|q|^2 + 1e-6)``); q is scaled by ``Dk^-1/2``.
+    """
+    _require(_is_int(chunk_size) and chunk_size in (1, 64), "chunk_size must be 1 or 64")
+    _require(isinstance(use_qk_l2norm_in_kernel, bool), "use_qk_l2norm_in_kernel must be bool")
+    gates_shape = tuple(query.shape[:3])
+    _require(query.ndim == 4 and key.shape == query.shape and value.ndim == 4
+             and tuple(value.shape[:3]) == gates_shape and tuple(g.shape) == gates_shape
+             and tuple(beta.shape) == gates_shape and min(query.shape) >= 1 and value.shape[-1] >= 1,
+             "GDN requires compatible [B,S,H,D] tensors and [B,S,H] gates")
     b, s, h, dk = query.shape
     dv = value.shape[-1]
-    if tuple(initial_state.shape) != (b, h, dk, dv) or initial_state.dtype not in (torch.float16, torch.float32):
-        raise ValueError("initial_state must be FP16/FP32 [B,H,Dk,Dv]")
-    if (effective_length.dtype != torch.int16 or tuple(effective_length.shape) != (b,)
-            or bool(((effective_length < 0) | (effective_length > s)).any())):
-        raise ValueError("effective_length must be INT16 [B] within [0,S]")
-    if query.dtype not in (torch.float16, torch.float32) or any(t.dtype != query.dtype for t in (key, value, g, beta)):
-        raise ValueError("GDN floating inputs must share FP16 or FP32 dtype")
-    q, k, v, decay, gate = (t.float() for t in (query, key, value, g, beta))
+    _require(tuple(initial_state.shape) == (b, h, dk, dv) and initial_state.dtype in (torch.float16, torch.float32),
+             "initial_state must be FP16/FP32 [B,H,Dk,Dv]")
+    _require(effective_length.dtype == torch.int16 and tuple(effective_length.shape) == (b,)
+             and bool(((effective_length >= 0) & (effective_length <= s)).all()),
+             "effective_length must be INT16 [B] within [0,S]")
+    _require(query.dtype in (torch.float16, torch.float32)
+             and all(t.dtype == query.dtype for t in (key, value, g, beta)),
+             "GDN floating inputs must share FP16 or FP32 dtype")
+    # head-major fp32 views [B, H, S, .]
+    q, k, v = (t.float().transpose(1, 2) for t in (query, key, value))
+    gf, bf = (t.float().transpose(1, 2) for t in (g, beta))
     if use_qk_l2norm_in_kernel:
-        q = q / torch.sqrt(q.pow(2).sum(-1, keepdim=True) + 1e-6)
-        k = k / torch.sqrt(k.pow(2).sum(-1, keepdim=True) + 1e-6)
-    q = q * (dk ** -0.5)
-    state = initial_state.float().clone()
-    length = effective_length.to(torch.int64)
+        q = q * (q.square().sum(-1, keepdim=True) + 1e-6).rsqrt()
+        k = k * (k.square().sum(-1, keepdim=True) + 1e-6).rsqrt()
+    q = q * dk ** -0.5
+    valid = (torch.arange(s, device=query.device)[None, :] < effective_length.to(torch.int64)[:, None])[:, None, :]
+    gf = torch.where(valid, gf, torch.zeros_like(gf))
+    bf = torch.where(valid, bf, torch.zeros_like(bf))
+    state = initial_state.float()
     outs = []
-    for i in range(s):
-        active = (i < length)[:, None, None, None]
-        st = state * torch.exp(decay[:, i])[:, :, None, None]
-        ki = k[:, i]
-        pred = (st * ki[:, :, :, None]).sum(dim=2)
-        delta = (v[:, i] - pred) * gate[:, i][:, :, None]
-        st = st + ki[:, :, :, None] * delta[:, :, None, :]
-        state = torch.where(active, st, state)
-        o = (state * q[:, i][:, :, :, None]).sum(dim=2)
-        outs.append(torch.where(active[..., 0], o, torch.zeros_like(o)))
-    return torch.stack(outs, dim=1).to(query.dtype), state.to(initial_state.dtype)
+    for c0 in range(0, s, 64):
+        c1 = min(s, c0 + 64)
+        out, state = _delta_rule_chunk(q[:, :, c0:c1], k[:, :, c0:c1], v[:, :, c0:c1], gf[:, :, c0:c1],
+                                       bf[:, :, c0:c1], state)
+        outs.append(out)
+    core = torch.cat(outs, dim=2) if len(outs) > 1 else outs[0]
+    core = torch.where(valid[..., None], core, torch.zeros_like(core))
+    return core.transpose(1, 2).to(query.dtype).contiguous(), state.to(initial_state.dtype)
 
 
 def cache_update(key: Optional[Tensor], value: Optional[Tensor], new_key: Tensor,
                  new_value: Tensor) -> tuple[Tensor, Tensor]:
-    """Append ``[B,Hkv,S,D]`` keys/values; returns new, privately owned caches."""
-    if ((key is None) != (value is None) or new_key.ndim != 4 or new_value.ndim != 4
-            or new_key.shape[:3] != new_value.shape[:3]):
-        raise ValueError("KV caches must appear together and use [B,H,T,D]")
+    """Append ``[B,Hkv,S,D]`` keys/values along the sequence axis; new, privately owned caches."""
+    _require((key is None) == (value is None) and new_key.ndim == 4 and new_value.ndim == 4
+             and new_key.shape[:3] == new_value.shape[:3],
+             "KV caches must appear together and use [B,H,T,D]")
     if key is None:
         return new_key.clone(), new_value.clone()
-    for old, new in ((key, new_key), (value, new_value)):
-        if old.ndim != 4 or old.shape[:2] != new.shape[:2] or old.shape[-1] != new.shape[-1] or old.dtype != new.dtype:
-            raise ValueError("old and new KV cache dimensions/dtypes do not match")
-    if key.shape[2] != value.shape[2]:
-        raise ValueError("old key and value cache lengths differ")
-    return torch.cat([key, new_key], dim=2), torch.cat([value, new_value], dim=2)
+    _require(all(old.ndim == 4 and old.shape[:2] == new.shape[:2] and old.shape[3] == new.shape[3]
+                 and old.dtype == new.dtype for old, new in ((key, new_key), (value, new_value))),
+             "old and new KV cache dimensions/dtypes do not match")
+    _require(key.shape[2] == value.shape[2], "old key and value cache lengths differ")
+    return torch.cat((key, new_key), dim=2), torch.cat((value, new_value), dim=2)
 
 
 def attention(query: Tensor, key: Tensor, value: Tensor, *, query_start: int, scale: float) -> Tensor:
-    """Causal GQA; query row i sees key positions ``<= query_start + i``.  fp32 math."""
-    if (query.ndim != 4 or key.ndim != 4 or value.ndim != 4 or query.shape[0] != key.shape[0]
-            or key.shape[:3] != value.shape[:3] or query.shape[-1] != key.shape[-1] or key.shape[1] < 1
-            or query.shape[1] % key.shape[1] or isinstance(query_start, bool) or not isinstance(query_start, int)
-            or query_start < 0 or query_start + query.shape[2] != key.shape[2]
-            or not math.isfinite(scale) or scale <= 0):
-        raise ValueError("attention requires causal append-only GQA [B,H,S,D] inputs")
-    rep = query.shape[1] // key.shape[1]
-    kf = key.float().repeat_interleave(rep, dim=1)
-    vf = value.float().repeat_interleave(rep, dim=1)
-    scores = torch.matmul(query.float(), kf.transpose(-1, -2).contiguous()) * scale
-    qpos = torch.arange(query.shape[2], device=query.device) + query_start
-    kpos = torch.arange(key.shape[2], device=query.device)
-    scores = scores.masked_fill((kpos[None, :] > qpos[:, None])[None, None], float("-inf"))
-    return torch.matmul(torch.softmax(scores, dim=-1), vf).to(query.dtype)
+    """Causal grouped-query attention in fp32: query row ``i`` sees key positions ``<= query_start + i``.
+
+    The ``H / Hkv`` query heads that share a KV head are stacked into one block of rows and
+    multiplied against that head's keys once, so the cache is never repeated per query head.
+    """
+    _require(query.ndim == 4 and key.ndim == 4 and value.ndim == 4 and query.shape[0] == key.shape[0]
+             and key.shape[:3] == value.shape[:3] and query.shape[3] == key.shape[3] and key.shape[1] >= 1
+             and query.shape[1] % key.shape[1] == 0 and _is_int(query_start) and query_start >= 0
+             and query_start + query.shape[2] == key.shape[2] and math.isfinite(scale) and scale > 0,
+             "attention requires causal append-only GQA [B,H,S,D] inputs")
+    b, heads, s, d = query.shape
+    kv, t = key.shape[1], key.shape[2]
+    group = heads // kv
+    rows = query.float().reshape(b, kv, group * s, d)               # query head kv*group + r -> rows r*s ..
+    keys_t = key.float().transpose(2, 3).contiguous()
+    scores = (rows @ keys_t) * scale                                 # [B, Hkv, group*S, T]
+    pos = torch.arange(s, device=query.device).repeat(group) + query_start
+    hidden = torch.arange(t, device=query.device)[None, :] > pos[:, None]
+    probs = torch.softmax(scores.masked_fill(hidden, -math.inf), dim=-1)
+    out = probs @ value.float()                                      # [B, Hkv, group*S, D]
+    return out.reshape(b, heads, s, d).to(query.dtype)
 
 
 # ------------------------------------------------------------------ hot path (HIP)

@@ -209,18 +209,43 @@ def _moe_common(hidden, gate_up: PackedW4, down: PackedW4, shared):
     return device, flat, sgu, sdn, sgate
 
 
+def _check_routing(routing: Routing, t: int, e: int, device: torch.device) -> int:
+    """Validate a caller-given routing against the layer (the kernels index with it); returns top_k."""
+    if not isinstance(routing, Routing):
+        raise ValueError("routing must be a Routing (ids, weights, perm, inv, offsets)")
+    ids = routing.ids
+    if not isinstance(ids, torch.Tensor) or ids.ndim != 2 or ids.shape[0] != t:
+        raise ValueError(f"routing.ids must be int32 [{t}, k]")
+    k = ids.shape[1]
+    if not 0 < k <= e:
+        raise ValueError(f"routing top_k must be in (0, {e}]")
+    expected = {"ids": (torch.int32, (t, k)), "weights": (torch.float32, (t, k)), "perm": (torch.int32, (t * k,)),
+                "inv": (torch.int32, (t * k,)), "offsets": (torch.int32, (e + 1,))}
+    for name, (dtype, shape) in expected.items():
+        v = getattr(routing, name)
+        if (not isinstance(v, torch.Tensor) or v.dtype != dtype or tuple(v.shape) != shape
+                or v.device != device or not v.is_contiguous()):
+            raise ValueError(f"routing.{name} must be a contiguous {dtype} {list(shape)} tensor on {device}")
+    return k
+
+
 def moe_experts(hidden: torch.Tensor, routing: Routing, gate_up: PackedW4, down: PackedW4, *,
                 shared: Optional[SharedExpert] = None, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Expert FFN + combine for a given routing; bf16 ``[T, H]``."""
+    """Expert FFN + combine for a given routing (as ``route`` returns it); bf16 ``[T, H]``.
+
+    The routing's arrays are checked for device, dtype, shape and contiguity;
+    their values are trusted (a routing not made by ``route`` must satisfy its
+    invariants: a permutation, offsets ascending from 0 to T*k).
+    """
     device, flat, sgu, sdn, sgate = _moe_common(hidden, gate_up, down, shared)
     t, h = flat.shape
-    k = routing.ids.shape[1] if routing.ids.ndim == 2 else 0
+    k = _check_routing(routing, t, gate_up.experts, device)
     out = torch.empty_like(flat)
     lib = _lib.load()
     ws = _workspace(lib.dflash_moe_workspace_bytes(t, h, gate_up.rows // 2, gate_up.experts, k, gate_up.group_size,
                                                    int(shared is not None)), device, workspace)
     gu, dn = _desc(gate_up), _desc(down)
-    _lib.call("dflash_moe_experts_w4a16", _ptr(flat), t, h, k, _ptr(routing.weights.contiguous()),
+    _lib.call("dflash_moe_experts_w4a16", _ptr(flat), t, h, k, _ptr(routing.weights),
               _ptr(routing.perm), _ptr(routing.inv), _ptr(routing.offsets), ctypes.byref(gu), ctypes.byref(dn),
               None if sgu is None else ctypes.byref(sgu), None if sdn is None else ctypes.byref(sdn), _ptr(sgate),
               _ptr(out), _ptr(ws), ws.numel(), _stream(device))

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import metrics, moe as oracle_moe
+from oracle import metrics, moe as oracle_moe, routing as oracle_routing
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-2
@@ -77,10 +77,63 @@ def test_moe_batch_of_blocks_skewed_t128(pkg, device):
 
 @pytest.mark.timeout(300)
 def test_moe_prefill_t2048(pkg, device):
-    """T=2048 uniform routing, every expert hit (~64 rows each)."""
-    print("moe T=2048", flush=True)
+    """T=2048 uniform routing, every expert hit (~64 rows each), on portable banks and on the
+    tiled banks the prefill workload runs on: both meet the bar and give identical bits."""
+    print("moe T=2048 portable", flush=True)
     layer = pkg.synthetic.moe_layer(2048, seed=4)
     _run_and_check(pkg, device, layer, 8)
+    print("moe T=2048 tiled", flush=True)
+    gu, dn, sh = _to(pkg, layer, device)
+    x, rw = layer.hidden.to(device), layer.router_weight.to(device)
+    out_p, r_p, _ = pkg.ops.moe_w4a16(x, gu, dn, top_k=8, router_weight=rw, shared=sh, return_routing=True)
+    out_t, r_t, _ = pkg.ops.moe_w4a16(x, gu.tiled(), dn.tiled(), top_k=8, router_weight=rw, shared=sh.tiled(),
+                                      return_routing=True)
+    assert torch.equal(r_p.perm, r_t.perm) and torch.equal(r_p.offsets, r_t.offsets)
+    assert torch.equal(out_p, out_t)
+
+
+def _logit_error_bound(hidden, router_weight):
+    """Worst-case error of an fp32 dot product of bf16 vectors (products exact in fp32, n-term
+    recursive sum): |err| <= n * 2^-24 / (1 - n * 2^-24) * sum|x_i w_i|, per (token, expert)."""
+    x = hidden.reshape(-1, hidden.shape[-1]).to(torch.float64).abs()
+    w = router_weight.to(torch.float64).abs()
+    n = hidden.shape[-1]
+    u = 2.0 ** -24
+    return (x @ w.T).numpy() * (n * u / (1 - n * u))
+
+
+@pytest.mark.parametrize("tokens,seed", [(16, 0), (128, 1), (2048, 4)])
+def test_routing_from_hidden_matches_oracle_logits(pkg, device, tokens, seed):
+    """End to end from (hidden, router_weight): the GPU's ids equal the oracle's ids computed on
+    the oracle's own logits (fp64 dot products rounded to fp32) on every row whose k+1 largest
+    logits are separated by more than twice the fp32 dot-product error bound -- there no
+    admissible fp32 summation order can change the selection or its order."""
+    print(f"routing end to end T={tokens}", flush=True)
+    k = 8
+    layer = pkg.synthetic.moe_layer(tokens, seed=seed)
+    x, rw = layer.hidden.to(device), layer.router_weight.to(device)
+    gu, dn, sh = _to(pkg, layer, device)
+    _, r, gpu_logits = pkg.ops.moe_w4a16(x, gu.tiled(), dn.tiled(), top_k=k, router_weight=rw, shared=sh.tiled(),
+                                         return_routing=True)
+    logits = oracle_moe.router_logits(layer.hidden, layer.router_weight)
+    bound = _logit_error_bound(layer.hidden, layer.router_weight)
+    assert np.all(np.abs(gpu_logits.cpu().numpy() - logits) <= bound + np.abs(logits) * 2.0 ** -23)
+    ids, wts = oracle_routing.topk(logits, k)
+    top = -np.sort(-logits, axis=1)[:, :k + 1]
+    sep = (top[:, :-1] - top[:, 1:]).min(axis=1) > 2 * bound.max(axis=1)
+    assert sep.mean() > 0.4, sep.mean()        # the seeds give 53-63% of rows; the check must cover many
+    got = r.ids.cpu().numpy()
+    np.testing.assert_array_equal(got[sep], ids[sep])
+    np.testing.assert_allclose(r.weights.cpu().numpy()[sep], wts[sep], rtol=0, atol=1e-5)
+    # every row: what the GPU selects lies within the error band of the oracle's k-th logit, and
+    # every expert clearly above the oracle's (k+1)-th logit is selected
+    band = 2 * bound.max(axis=1)
+    chosen = np.take_along_axis(logits, got.astype(np.int64), axis=1)
+    assert np.all(chosen >= (top[:, k - 1] - band)[:, None])
+    for t in range(tokens):
+        clear = set(np.nonzero(logits[t] > top[t, k] + band[t])[0].tolist())
+        assert clear <= set(got[t].tolist()), t
+    print(f"  rows checked bit-exactly: {int(sep.sum())} of {tokens}", flush=True)
 
 
 @pytest.mark.parametrize("tokens,experts,k,hidden,inter,group,scale_dtype,shared", [

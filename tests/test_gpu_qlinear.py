@@ -95,13 +95,27 @@ def test_qlinear_stacked_projections(pkg, device, layout):
         col += n
 
 
-@pytest.mark.parametrize("m", [5, 16, 24])
-def test_qlinear_k4096_row_counts(pkg, device, m):
-    """K = 4096 runs the verify kernel up to 16 rows and the streaming kernels above."""
+@pytest.mark.parametrize("m", [5, 16, 17, 24, 32, 33])
+@pytest.mark.parametrize("layout", ["portable", "tiled"])
+def test_qlinear_k4096_row_counts(pkg, device, m, layout):
+    """K = 4096: the verify kernel stages at most 16 rows, so 17..32 rows run as two launches of
+    16 (row 16 is the first row of the second launch); above 32 rows the portable layout takes
+    the per-wave kernel and the tiled layout is refused (no kernel streams it at that shape)."""
+    print(f"qlinear K=4096 m={m} {layout}", flush=True)
     x, weight = _case(pkg, m, 256, 4096, 128, torch.bfloat16, seed=m)
-    y = pkg.ops.qlinear(x.to(device), weight.to(device)).cpu()
+    w = weight.to(device)
+    if layout == "tiled":
+        w = w.tiled()
+        if m > 32:
+            with pytest.raises(pkg._lib.DflashError, match="tiled"):
+                pkg.ops.qlinear(x.to(device), w)
+            return
+    y = pkg.ops.qlinear(x.to(device), w).cpu()
     report = metrics.compare(y, w4.qlinear(x, weight.packed.numpy(), weight.scales, 128))
     assert report["max_rel"] <= TOL and report["cosine"] > 0.9999, report
+    if m > 16 and m <= 32:   # every row, the first of the second launch included, is right on its own
+        rows = metrics.compare(y[16:17], w4.qlinear(x[16:17], weight.packed.numpy(), weight.scales, 128))
+        assert rows["max_rel"] <= TOL, rows
 
 
 def test_qlinear_lm_head(pkg, device):

@@ -210,3 +210,44 @@ def test_measure_stage_validation(pkg):
     assert lib.dflash_set_measure_stage(7) == 1
     assert "stage" in lib.dflash_last_error().decode()
     assert lib.dflash_set_measure_stage(0) == 0
+
+
+def test_moe_experts_refuses_malformed_routing(pkg):
+    """A caller-given routing is checked for dtype, shape, device and contiguity before its
+    pointers reach the kernels (they index the work table and the weights with it)."""
+    import torch
+    t, e, k = 4, 16, 2
+    cpu = torch.device("cpu")
+
+    def routing(**over):
+        parts = dict(ids=torch.zeros((t, k), dtype=torch.int32), weights=torch.zeros((t, k)),
+                     perm=torch.arange(t * k, dtype=torch.int32), inv=torch.arange(t * k, dtype=torch.int32),
+                     offsets=torch.zeros(e + 1, dtype=torch.int32))
+        parts.update(over)
+        return pkg.ops.Routing(**parts)
+
+    assert pkg.ops._check_routing(routing(), t, e, cpu) == k
+    bad = {
+        "perm": torch.arange(t * k, dtype=torch.int64),                 # int64 permutation
+        "offsets": torch.zeros(e, dtype=torch.int32),                   # one offset short
+        "weights": torch.zeros((t, k), dtype=torch.bfloat16),           # not fp32
+        "inv": torch.arange(2 * t * k, dtype=torch.int32)[::2],         # strided view
+        "ids": torch.zeros((t + 1, k), dtype=torch.int32),              # wrong token count
+    }
+    for name, value in bad.items():
+        with pytest.raises(ValueError, match=f"routing.{name}|routing top_k|ids"):
+            pkg.ops._check_routing(routing(**{name: value}), t, e, cpu)
+    with pytest.raises(ValueError, match="on meta"):
+        pkg.ops._check_routing(routing(), t, e, torch.device("meta"))
+    with pytest.raises(ValueError, match="top_k"):
+        pkg.ops._check_routing(routing(ids=torch.zeros((t, e + 1), dtype=torch.int32)), t, e, cpu)
+    with pytest.raises(ValueError, match="Routing"):
+        pkg.ops._check_routing(tuple(routing()), t, e, cpu)
+
+
+@host_only
+def test_route_caps_tokens_times_top_k(pkg):
+    """T * k above 2^28 is refused before any launch (32-bit routing offsets)."""
+    p = ctypes.c_void_p(16)
+    st, msg = _status(pkg, "dflash_moe_route", p, 1 << 23, 1024, 64, p, p, p, p, p, p, 1 << 40, None)
+    assert st == 2 and "2^28" in msg
