@@ -23,7 +23,7 @@ from typing import Optional
 import torch
 from torch import Tensor
 
-from . import ops
+from . import layers, ops
 from .packing import PackedW4, SharedExpert
 
 FUSED_OPS_ABI = 1
@@ -91,43 +91,15 @@ def causal_conv1d(padded: Tensor, weight: Tensor) -> Tensor:
     return out.to(padded.dtype).transpose(1, 2).contiguous()
 
 
-def _delta_rule_chunk(q, k, v, g, beta, state):
-    """One chunk of the gated delta rule in closed (WY) form, fp32, batched over [B, H].
-
-    With ``G_t = sum_{s<=t} g_s`` the recurrence ``S_t = e^{g_t} S_{t-1} + k_t u_t^T``,
-    ``u_t = beta_t (v_t - e^{g_t} S_{t-1}^T k_t)`` unrolls to the unit lower-triangular
-    system ``(I + A) U = diag(beta) (V - diag(e^G) K S_0)`` with
-    ``A_ts = beta_t e^{G_t - G_s} k_t.k_s`` (s < t); then
-    ``o_t = e^{G_t} S_0^T q_t + sum_{s<=t} e^{G_t - G_s} (q_t.k_s) u_s`` and
-    ``S_C = e^{G_C} S_0 + sum_s e^{G_C - G_s} k_s u_s^T``.  Every decay factor used is
-    ``e^{G_t - G_s}`` with ``s <= t`` (at most 1): no overflow for long chunks.
-    Shapes: q, k ``[B,H,C,Dk]``, v ``[B,H,C,Dv]``, g, beta ``[B,H,C]``, state ``[B,H,Dk,Dv]``.
-    """
-    c = q.shape[2]
-    cum = torch.cumsum(g, dim=-1)                                   # G_t
-    diff = cum[..., :, None] - cum[..., None, :]                    # G_t - G_s
-    causal = torch.ones((c, c), dtype=torch.bool, device=q.device).tril()
-    decay = torch.where(causal, diff, torch.full_like(diff, -math.inf)).exp()   # 0 above the diagonal
-    strict = (decay * (k @ k.transpose(-1, -2)) * beta[..., :, None]).tril(-1)
-    head = cum.exp()[..., None]                                     # e^{G_t}
-    rhs = beta[..., None] * (v - head * (k @ state))
-    eye = torch.eye(c, dtype=q.dtype, device=q.device)
-    u = torch.linalg.solve_triangular(eye + strict, rhs, upper=False, unitriangular=True)
-    out = head * (q @ state) + (decay * (q @ k.transpose(-1, -2))) @ u
-    tail = (cum[..., -1:] - cum).exp()[..., None]                   # e^{G_C - G_s}
-    new_state = cum[..., -1:, None].exp() * state + (k * tail).transpose(-1, -2) @ u
-    return out, new_state
-
-
 def chunk_gated_delta_rule(query: Tensor, key: Tensor, value: Tensor, g: Tensor, beta: Tensor,
                            initial_state: Tensor, effective_length: Tensor, *, chunk_size: int,
                            use_qk_l2norm_in_kernel: bool) -> tuple[Tensor, Tensor]:
     """Gated delta rule over ``[B,S,H,D]`` tokens; returns core ``[B,S,H,Dv]`` and the final state.
 
     Tokens at or past ``effective_length[b]`` leave the state unchanged and output zeros
-    (they enter the chunk with ``g = 0`` and ``beta = 0``).  Math in fp32, chunks of 64
-    tokens (``chunk_size`` is the caller's decode/prefill tag, 1 or 64; the closed chunk
-    form is exact for any length).  Q/K are L2-normalised here when asked to be
+    (they enter the chunk with ``g = 0`` and ``beta = 0``).  Math in fp32, in closed-form
+    chunks of 16 tokens (``layers.delta_rule``; ``chunk_size`` is the caller's decode/prefill
+    tag, 1 or 64, and does not change the result).  Q/K are L2-normalised here when asked to be
     (``q / sqrt(|q|^2 + 1e-6)``); q is scaled by ``Dk^-1/2``.
     """
     _require(_is_int(chunk_size) and chunk_size in (1, 64), "chunk_size must be 1 or 64")
@@ -147,25 +119,11 @@ def chunk_gated_delta_rule(query: Tensor, key: Tensor, value: Tensor, g: Tensor,
     _require(query.dtype in (torch.float16, torch.float32)
              and all(t.dtype == query.dtype for t in (key, value, g, beta)),
              "GDN floating inputs must share FP16 or FP32 dtype")
-    # head-major fp32 views [B, H, S, .]
-    q, k, v = (t.float().transpose(1, 2) for t in (query, key, value))
-    gf, bf = (t.float().transpose(1, 2) for t in (g, beta))
-    if use_qk_l2norm_in_kernel:
-        q = q * (q.square().sum(-1, keepdim=True) + 1e-6).rsqrt()
-        k = k * (k.square().sum(-1, keepdim=True) + 1e-6).rsqrt()
-    q = q * dk ** -0.5
+    # head-major fp32 [B, H, S, .]; layers.delta_rule normalises, scales q and chunks
+    q, k, v, gf, bf = (t.float().transpose(1, 2) for t in (query, key, value, g, beta))
     valid = (torch.arange(s, device=query.device)[None, :] < effective_length.to(torch.int64)[:, None])[:, None, :]
-    gf = torch.where(valid, gf, torch.zeros_like(gf))
-    bf = torch.where(valid, bf, torch.zeros_like(bf))
-    state = initial_state.float()
-    outs = []
-    for c0 in range(0, s, 64):
-        c1 = min(s, c0 + 64)
-        out, state = _delta_rule_chunk(q[:, :, c0:c1], k[:, :, c0:c1], v[:, :, c0:c1], gf[:, :, c0:c1],
-                                       bf[:, :, c0:c1], state)
-        outs.append(out)
-    core = torch.cat(outs, dim=2) if len(outs) > 1 else outs[0]
-    core = torch.where(valid[..., None], core, torch.zeros_like(core))
+    core, state, _ = layers.delta_rule(q, k, v, gf, bf, initial_state.float(), normalise=use_qk_l2norm_in_kernel,
+                                       valid=valid)
     return core.transpose(1, 2).to(query.dtype).contiguous(), state.to(initial_state.dtype)
 
 
@@ -195,17 +153,7 @@ def attention(query: Tensor, key: Tensor, value: Tensor, *, query_start: int, sc
              and query.shape[1] % key.shape[1] == 0 and _is_int(query_start) and query_start >= 0
              and query_start + query.shape[2] == key.shape[2] and math.isfinite(scale) and scale > 0,
              "attention requires causal append-only GQA [B,H,S,D] inputs")
-    b, heads, s, d = query.shape
-    kv, t = key.shape[1], key.shape[2]
-    group = heads // kv
-    rows = query.float().reshape(b, kv, group * s, d)               # query head kv*group + r -> rows r*s ..
-    keys_t = key.float().transpose(2, 3).contiguous()
-    scores = (rows @ keys_t) * scale                                 # [B, Hkv, group*S, T]
-    pos = torch.arange(s, device=query.device).repeat(group) + query_start
-    hidden = torch.arange(t, device=query.device)[None, :] > pos[:, None]
-    probs = torch.softmax(scores.masked_fill(hidden, -math.inf), dim=-1)
-    out = probs @ value.float()                                      # [B, Hkv, group*S, D]
-    return out.reshape(b, heads, s, d).to(query.dtype)
+    return layers.grouped_attention(query, key, value, query_start, scale).to(query.dtype)
 
 
 # ------------------------------------------------------------------ hot path (HIP)
