@@ -5,8 +5,9 @@
  * stream-ordered on the caller's HIP stream (passed as void*), never
  * allocates or frees device memory, never synchronises, and keeps no pointer
  * after it returns.  Scratch memory is a caller-provided workspace whose size
- * comes from the matching *_workspace_bytes() query.  Device pointers must be
- * 16-byte aligned.
+ * comes from the matching *_workspace_bytes() query, except for
+ * dflash_moe_w4a16_noalloc, whose scratch is a static per-device array of the
+ * library.  Device pointers must be 16-byte aligned.
  *
  * Weight format (reference model/qwen35_moe_dflash/graph/quant_weights.py:147-148,
  * graph/quant_plan.py:76-87,165): a logical weight W[E][N][K] is stored as
@@ -28,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DFLASH_ABI_VERSION 3
+#define DFLASH_ABI_VERSION 4
 
 enum dflash_status {
   DFLASH_OK = 0,
@@ -172,6 +173,24 @@ int dflash_moe_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, co
                      void* out, float* logits_out, int32_t* topk_ids, float* topk_weights, int32_t* perm,
                      int32_t* inv_perm, int32_t* expert_offsets, void* workspace, size_t workspace_bytes,
                      void* stream);
+
+/*
+ * dflash_moe_w4a16 without a workspace: the same layer, arguments and results, with its
+ * scratch in a static device array of DFLASH_NOALLOC_SCRATCH_BYTES (8 MiB) that each GPU
+ * the library runs on holds until the process ends.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  It calls no allocating routine.
+ * A layer whose dflash_moe_workspace_bytes() exceeds the scratch is refused with
+ * DFLASH_ERR_UNSUPPORTED (at H=2048, I=512, E=256, top-8 + shared expert: up to 92 tokens).
+ * All calls on one GPU share its scratch: calls that overlap on one GPU race.
+ */
+#define DFLASH_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
+int dflash_moe_w4a16_noalloc(const void* hidden, int64_t tokens, int64_t hidden_size, const float* router_logits,
+                             const void* router_weight, int64_t top_k, const dflash_w4* gate_up,
+                             const dflash_w4* down, const dflash_w4* shared_gate_up, const dflash_w4* shared_down,
+                             const void* shared_gate_weight, void* out, float* logits_out, int32_t* topk_ids,
+                             float* topk_weights, int32_t* perm, int32_t* inv_perm, int32_t* expert_offsets,
+                             void* stream);
 
 /*
  * Measurement mode (no counterpart in the reference; for benchmarks and

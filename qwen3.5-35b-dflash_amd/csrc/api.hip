@@ -5,6 +5,7 @@
 // synchronisation, no C++ exception crosses the ABI.
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 #include <string>
 
 #include "../../include/dflash_hip.h"
@@ -123,6 +124,36 @@ MoeLayout moe_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, bool
 template <typename T>
 T* at(void* base, size_t off) {
   return reinterpret_cast<T*>(static_cast<char*>(base) + off);
+}
+
+// Scratch of dflash_moe_w4a16_noalloc: one copy per device, held until the process ends.
+// In host code `scratch` names a host-side stand-in, never the device memory: kernels and
+// copies get the address that hipGetSymbolAddress returns for the current device.  Every
+// call on a device shares that device's copy, so calls that overlap on one device race;
+// each call's kernels clear what must start at zero (routing counters, slot map, tile
+// queues) before using it.
+constexpr size_t kScratchBytes = DFLASH_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_on_current_device(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(DFLASH_ERR_HIP, std::string("hipGetDevice: ") + hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(DFLASH_ERR_UNSUPPORTED, "device index above 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(DFLASH_ERR_HIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return DFLASH_OK;
 }
 
 // Compute units of the current device (persistent grids launch one workgroup per CU).
@@ -764,12 +795,14 @@ int dflash_moe_experts_w4a16(const void* hidden, int64_t tokens, int64_t hidden_
   }
 }
 
-int dflash_moe_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, const float* router_logits,
-                     const void* router_weight, int64_t top_k, const dflash_w4* gate_up, const dflash_w4* down,
-                     const dflash_w4* shared_gate_up, const dflash_w4* shared_down, const void* shared_gate_weight,
-                     void* out, float* logits_out, int32_t* topk_ids, float* topk_weights, int32_t* perm,
-                     int32_t* inv_perm, int32_t* expert_offsets, void* workspace, size_t workspace_bytes,
-                     void* stream) {
+// The whole layer on a caller workspace, or (static_scratch) on this device's copy of
+// `scratch`, whose address is looked up only after every argument has been validated.
+static int moe_w4a16_body(const void* hidden, int64_t tokens, int64_t hidden_size, const float* router_logits,
+                          const void* router_weight, int64_t top_k, const dflash_w4* gate_up, const dflash_w4* down,
+                          const dflash_w4* shared_gate_up, const dflash_w4* shared_down,
+                          const void* shared_gate_weight, void* out, float* logits_out, int32_t* topk_ids,
+                          float* topk_weights, int32_t* perm, int32_t* inv_perm, int32_t* expert_offsets,
+                          void* workspace, size_t workspace_bytes, bool static_scratch, void* stream) {
   try {
     MoeShapes S;
     if (int r = check_moe(hidden, tokens, hidden_size, top_k, gate_up, down, shared_gate_up, shared_down,
@@ -783,6 +816,14 @@ int dflash_moe_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, co
     if (tokens > 0 && (!topk_ids || !topk_weights || !perm || !inv_perm))
       return fail(DFLASH_ERR_INVALID_ARGUMENT, "routing output arrays are required");
     const MoeLayout L = moe_layout(S.T, S.H, S.I, S.E, S.k, S.shared);
+    if (static_scratch) {
+      if (L.total > kScratchBytes)
+        return fail(DFLASH_ERR_UNSUPPORTED, "moe_noalloc: this layer needs " + std::to_string(L.total) +
+                                                " bytes of scratch, above the static " +
+                                                std::to_string(kScratchBytes) + "; use dflash_moe_w4a16");
+      if (int r = scratch_on_current_device(&workspace)) return r;
+      workspace_bytes = kScratchBytes;
+    }
     if (!workspace || workspace_bytes < L.total || !aligned16(workspace))
       return fail(DFLASH_ERR_WORKSPACE, "moe workspace needs " + std::to_string(L.total) + " bytes");
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -830,6 +871,28 @@ int dflash_moe_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, co
   } catch (...) {
     return fail(DFLASH_ERR_HIP, "unexpected host exception");
   }
+}
+
+int dflash_moe_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, const float* router_logits,
+                     const void* router_weight, int64_t top_k, const dflash_w4* gate_up, const dflash_w4* down,
+                     const dflash_w4* shared_gate_up, const dflash_w4* shared_down, const void* shared_gate_weight,
+                     void* out, float* logits_out, int32_t* topk_ids, float* topk_weights, int32_t* perm,
+                     int32_t* inv_perm, int32_t* expert_offsets, void* workspace, size_t workspace_bytes,
+                     void* stream) {
+  return moe_w4a16_body(hidden, tokens, hidden_size, router_logits, router_weight, top_k, gate_up, down,
+                        shared_gate_up, shared_down, shared_gate_weight, out, logits_out, topk_ids, topk_weights,
+                        perm, inv_perm, expert_offsets, workspace, workspace_bytes, false, stream);
+}
+
+int dflash_moe_w4a16_noalloc(const void* hidden, int64_t tokens, int64_t hidden_size, const float* router_logits,
+                             const void* router_weight, int64_t top_k, const dflash_w4* gate_up,
+                             const dflash_w4* down, const dflash_w4* shared_gate_up, const dflash_w4* shared_down,
+                             const void* shared_gate_weight, void* out, float* logits_out, int32_t* topk_ids,
+                             float* topk_weights, int32_t* perm, int32_t* inv_perm, int32_t* expert_offsets,
+                             void* stream) {
+  return moe_w4a16_body(hidden, tokens, hidden_size, router_logits, router_weight, top_k, gate_up, down,
+                        shared_gate_up, shared_down, shared_gate_weight, out, logits_out, topk_ids, topk_weights,
+                        perm, inv_perm, expert_offsets, nullptr, 0, true, stream);
 }
 
 int dflash_set_measure_stage(int stage) {

@@ -296,6 +296,61 @@ def moe_w4a16(hidden: torch.Tensor, gate_up: PackedW4, down: PackedW4, *, top_k:
     return out
 
 
+NOALLOC_SCRATCH_BYTES = 8 << 20
+
+
+def moe_w4a16_noalloc(hidden: torch.Tensor, gate_up: PackedW4, down: PackedW4, *, top_k: int,
+                      router_weight: Optional[torch.Tensor] = None, router_logits: Optional[torch.Tensor] = None,
+                      shared: Optional[SharedExpert] = None, out: Optional[torch.Tensor] = None,
+                      routing: Optional[Routing] = None, logits_out: Optional[torch.Tensor] = None):
+    """``moe_w4a16`` through ``dflash_moe_w4a16_noalloc``: no workspace, the library's static scratch.
+
+    The library allocates nothing; this wrapper allocates the outputs only when the caller
+    does not pass them (``out`` bf16 ``[T, H]``, ``routing`` buffers, ``logits_out`` fp32
+    ``[T, E]``).  Returns ``(out, routing, logits)``.  Layers needing more than
+    ``NOALLOC_SCRATCH_BYTES`` of scratch raise :class:`DflashError`.
+    """
+    device, flat, sgu, sdn, sgate = _moe_common(hidden, gate_up, down, shared)
+    if type(top_k) is not int:
+        raise ValueError("top_k must be an int")
+    t, h = flat.shape
+    e = gate_up.experts
+    if router_logits is not None:
+        _require_device(router_logits)
+        if router_logits.dtype != torch.float32 or tuple(router_logits.shape) != (t, e):
+            raise ValueError(f"router_logits must be float32 [{t}, {e}]")
+        router_logits = router_logits.contiguous()
+        logits_out = router_logits
+    else:
+        if router_weight is None:
+            raise ValueError("router_weight or router_logits is required")
+        _require_device(router_weight)
+        if router_weight.dtype != torch.bfloat16 or tuple(router_weight.shape) != (e, h):
+            raise ValueError(f"router_weight must be bfloat16 [{e}, {h}]")
+        router_weight = router_weight.contiguous()
+        if logits_out is None:
+            logits_out = torch.empty((t, e), dtype=torch.float32, device=device)
+        elif (logits_out.dtype != torch.float32 or tuple(logits_out.shape) != (t, e) or logits_out.device != device
+              or not logits_out.is_contiguous()):
+            raise ValueError(f"logits_out must be a contiguous float32 [{t}, {e}] tensor on {device}")
+    if routing is None:
+        routing = _routing_buffers(t, e, top_k, device)
+    elif _check_routing(routing, t, e, device) != top_k:
+        raise ValueError("routing buffers must hold top_k slots per token")
+    if out is None:
+        out = torch.empty_like(flat)
+    elif out.dtype != torch.bfloat16 or tuple(out.shape) != (t, h) or out.device != device or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous bfloat16 [{t}, {h}] tensor on {device}")
+    gu, dn = _desc(gate_up), _desc(down)
+    r = routing
+    _lib.call("dflash_moe_w4a16_noalloc", _ptr(flat), t, h, _ptr(router_logits), _ptr(router_weight), top_k,
+              ctypes.byref(gu), ctypes.byref(dn), None if sgu is None else ctypes.byref(sgu),
+              None if sdn is None else ctypes.byref(sdn), _ptr(sgate), _ptr(out),
+              None if router_logits is not None else _ptr(logits_out), _ptr(r.ids), _ptr(r.weights), _ptr(r.perm),
+              _ptr(r.inv), _ptr(r.offsets), _stream(device))
+    return out, routing, logits_out
+
+
 def qlinear_workspace_bytes(m: int, k: int, group_size: int = 128) -> int:
     return int(_lib.load().dflash_qlinear_workspace_bytes(m, k, group_size))
 

@@ -28,7 +28,7 @@ def test_library_loads_and_exports_every_symbol(pkg):
     lib = pkg._lib.load()
     for name in _declared_functions():
         assert hasattr(lib, name), name
-    assert lib.dflash_abi_version() == pkg._lib.ABI_VERSION == 3
+    assert lib.dflash_abi_version() == pkg._lib.ABI_VERSION == 4
 
 
 def test_library_has_no_unresolved_internal_symbols(pkg):
@@ -251,3 +251,18 @@ def test_route_caps_tokens_times_top_k(pkg):
     p = ctypes.c_void_p(16)
     st, msg = _status(pkg, "dflash_moe_route", p, 1 << 23, 1024, 64, p, p, p, p, p, p, 1 << 40, None)
     assert st == 2 and "2^28" in msg
+
+
+@host_only
+def test_noalloc_refuses_oversized_layers_before_any_launch(pkg):
+    """dflash_moe_w4a16_noalloc: a layer whose scratch exceeds the static array is refused on
+    the host (status 2) before the array's address is even looked up."""
+    p = ctypes.c_void_p(16)
+    gu = _desc(pkg, experts=256, rows=1024, cols=2048)
+    dn = _desc(pkg, experts=256, rows=2048, cols=512)
+    lib = pkg._lib.load()
+    assert lib.dflash_moe_workspace_bytes(2048, 2048, 512, 256, 8, 128, 0) > 8 << 20
+    st = lib.dflash_moe_w4a16_noalloc(p, 2048, 2048, None, p, 8, ctypes.byref(gu), ctypes.byref(dn), None, None,
+                                      None, p, None, p, p, p, p, p, None)
+    assert st == 2 and "scratch" in lib.dflash_last_error().decode()
+    assert lib.dflash_moe_workspace_bytes(16, 2048, 512, 256, 8, 128, 1) <= 8 << 20
