@@ -248,6 +248,55 @@ def time_stage(pkg, sets, blocks, top_k, steps, warmup, stage=None, given_logits
     return ms, statistics.mean(hits)
 
 
+def time_stack(pkg, device, steps, warmup, context=4096, tokens=16):
+    """The 40-layer target's verify forward over a 16-token block at a 4096-token context.
+
+    Step = embedding, 30 GDN + 10 attention layers (each: norm, mixer, norm, routed MoE with
+    the shared expert), final norm, LM head and top-1, replayed from HIP graphs (period 4).
+    ``kernel_share`` = time of the same qlinear + MoE launches alone (the same shapes, in a
+    graph of their own) / time of the whole forward.
+    """
+    c = pkg.plan.TargetConfig()
+    w = pkg.target.random_weights(c, seed=7, device=device)
+    model = pkg.target.TargetModel(w, capacity=context + 64, feature_layers=pkg.target.DRAFT_FEATURE_LAYERS)
+    state = model.synthetic_context(context, seed=8)
+    gen = torch.Generator(device=device).manual_seed(9)
+    ids = torch.randint(0, c.vocab, (tokens,), device=device, generator=gen)
+    ws = torch.empty(pkg.ops.moe_workspace_bytes(tokens, c.hidden, c.moe_inter, c.experts, c.top_k, 128, True),
+                     dtype=torch.uint8, device=device)
+    torch.cuda.synchronize()
+    full_ms = time_steps(lambda j: model.forward(ids, state, workspace=ws), steps, warmup, period=4)
+    hidden = model.embed(ids)
+    gdn_ms = time_steps(lambda j: model.layer(0, hidden, state, ws), steps, warmup, period=8)
+    attn_ms = time_steps(lambda j: model.layer(3, hidden, state, ws), steps, warmup, period=8)
+    head_ms = time_steps(lambda j: pkg.ops.qlinear(hidden.to(torch.bfloat16), w.lm_head).argmax(-1), steps, warmup,
+                         period=8)
+    x = torch.randn((tokens, c.hidden), device=device, generator=gen).to(torch.bfloat16)
+    x_gdn = torch.randn((tokens, c.linear_value_heads * c.linear_value_dim), device=device,
+                        generator=gen).to(torch.bfloat16)
+    x_att = torch.randn((tokens, c.heads * c.head_dim), device=device, generator=gen).to(torch.bfloat16)
+
+    def kernels_only(j):
+        for lw in w.layers:
+            pkg.ops.qlinear(x, lw.mixer_in)
+            pkg.ops.qlinear(x_gdn if lw.kind == "linear_attention" else x_att, lw.mixer_out)
+            pkg.ops.moe_w4a16(x, lw.gate_up, lw.down, top_k=c.top_k, router_weight=lw.router, shared=lw.shared,
+                              workspace=ws)
+        pkg.ops.qlinear(x, w.lm_head)
+    kern_ms = time_steps(kernels_only, steps, warmup, period=4)
+    n_gdn = sum(k == "linear_attention" for k in c.layer_types)
+    del model, w, state
+    torch.cuda.empty_cache()
+    return {"workload": f"40-layer target verify forward: T={tokens} over a {context}-token context, batch 1 "
+                        "(30 GDN + 10 attention layers, 256 experts top-8 + shared, all projections, experts and "
+                        "the LM head W4A16 g128 tiled; router bf16); embedding through LM head top-1",
+            "us_total": round(full_ms * 1e3, 1), "us_per_layer": round((full_ms - head_ms) * 1e3 / c.layers, 1),
+            "us_gdn_layer": round(gdn_ms * 1e3, 1), "us_attention_layer": round(attn_ms * 1e3, 1),
+            "us_lm_head": round(head_ms * 1e3, 1), "gdn_layers": n_gdn, "attention_layers": c.layers - n_gdn,
+            "us_kernels_only": round(kern_ms * 1e3, 1), "kernel_share": round(kern_ms / full_ms, 3),
+            "steps": steps, "graph_period": 4}
+
+
 def measured_traffic():
     """HBM bytes per gate/up launch from the committed counter passes, or None."""
     path = ROOT / "profiles" / "hbm_traffic_gate_up_t16.json"
@@ -304,6 +353,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-qlinear", action="store_true")
+    ap.add_argument("--no-stack", action="store_true")
+    ap.add_argument("--only-stack", action="store_true", help="time the 40-layer stack only (no JSON metric line)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (reference dispatch for HBM byte counters)")
     args = ap.parse_args()
@@ -316,6 +367,9 @@ def main() -> int:
     device = torch.device("cuda:0")
     pkg._lib.load()
     top_k, tokens = 8, 16
+    if args.only_stack:
+        print(json.dumps({"stack": time_stack(pkg, device, max(8, args.steps // 10), max(4, args.warmup // 5))}))
+        return 0
 
     log("generating weight sets on the device")
     sets = weight_sets(pkg, args.sets, device)
@@ -379,6 +433,9 @@ def main() -> int:
         tflops = moe_flops(2048, top_k) / (ms_p * 1e-3) / 1e12
         result["prefill"] = {"tokens": 2048, "us_per_layer": round(ms_p * 1e3, 1), "tflops": round(tflops, 2),
                              "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4), "steps": steps_p}
+    if not args.no_stack:
+        log("timing the 40-layer verify stack")
+        result["stack"] = time_stack(pkg, device, max(8, args.steps // 10), max(4, args.warmup // 5))
     if not args.no_qlinear:
         log("timing the qlinear projections and the LM head")
         result["qlinear"] = time_qlinear(pkg, device, max(24, args.steps // 2), args.warmup)

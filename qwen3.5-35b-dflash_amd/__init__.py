@@ -7,9 +7,12 @@ The directory name is not a Python identifier; load it under the alias
 * ``fused_ops`` -- FusedOps ABI-v1 adapter module (the drop-in seam)
 * ``ops``       -- PyTorch-ROCm wrappers over the C ABI
 * ``packing``   -- ``PackedW4`` / ``SharedExpert`` types and the int4 packer
+* ``plan``      -- tensor inventory of the target (names, shapes, which are int4)
+* ``layers``    -- non-hot decoder arithmetic (delta rule, norms, rotary, attention)
+* ``target``    -- the verify forward of the whole target on the HIP kernels
 * ``synthetic`` -- seeded synthetic workloads (tests and benchmark)
 * ``_lib``      -- ctypes binding of ``libdflash_hip.so``
 * ``build``     -- hipcc build recipe
 """
-from . import _lib, fused_ops, ops, packing, synthetic  # noqa: F401
+from . import _lib, fused_ops, layers, ops, packing, plan, synthetic, target  # noqa: F401
 from .packing import PackedW4, SharedExpert, concat_rows, pack_int4, quantize_w4  # noqa: F401

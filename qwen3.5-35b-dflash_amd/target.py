@@ -141,6 +141,23 @@ def random_weights(config: TargetConfig, *, seed: int = 0, device="cuda", layout
     return out
 
 
+def to_device(w: TargetWeights, device, *, layout: str = "tiled") -> TargetWeights:
+    """A copy of ``w`` on ``device``, every packed bank in ``layout``."""
+    def move(v):
+        if isinstance(v, PackedW4):
+            b = v.to(device)
+            return b.tiled() if layout == "tiled" and b.layout != "tiled" else b
+        if isinstance(v, SharedExpert):
+            return SharedExpert(move(v.gate_up), move(v.down), v.gate_weight.to(device))
+        if isinstance(v, Tensor):
+            return v.to(device)
+        return v
+    out = TargetWeights(w.config, move(w.embedding), move(w.embedding_scale), move(w.final_norm), move(w.lm_head))
+    for lw in w.layers:
+        out.layers.append(LayerWeights(**{k: move(v) for k, v in vars(lw).items()}))
+    return out
+
+
 # ------------------------------------------------------------------ state
 @dataclass
 class TargetState:
@@ -286,8 +303,10 @@ class TargetModel:
         return ops.moe_w4a16(x, lw.gate_up, lw.down, top_k=self.config.top_k, router_weight=lw.router,
                              shared=lw.shared, workspace=workspace)
 
-    def layer(self, i: int, hidden: Tensor, state: TargetState, workspace: Optional[Tensor] = None):
-        """One decoder layer on the fp32 residual ``[T, H]``; returns (hidden, GdnPending or None)."""
+    def layer(self, i: int, hidden: Tensor, state: TargetState, workspace: Optional[Tensor] = None,
+              trace: Optional[dict] = None):
+        """One decoder layer on the fp32 residual ``[T, H]``; returns (hidden, GdnPending or None).
+        ``trace`` (a dict) receives the residual after the mixer and the MoE input."""
         c, lw = self.config, self.w.layers[i]
         normed = layers.rms_normalise(hidden, lw.input_norm, c.rms_eps, 1.0).to(torch.bfloat16)
         pending = None
@@ -297,6 +316,8 @@ class TargetModel:
             mixed = self._attention(normed, lw, state.keys[i], state.values[i], state.position)
         hidden = hidden + mixed.float()
         normed = layers.rms_normalise(hidden, lw.post_norm, c.rms_eps, 1.0).to(torch.bfloat16)
+        if trace is not None:
+            trace.update(mid=hidden, moe_in=normed)
         return hidden + self._moe(normed, lw, workspace).float(), pending
 
     def forward_hidden(self, hidden: Tensor, state: TargetState, *, top1: bool = True,
