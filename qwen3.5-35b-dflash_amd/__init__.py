@@ -10,9 +10,11 @@ The directory name is not a Python identifier; load it under the alias
 * ``plan``      -- tensor inventory of the target (names, shapes, which are int4)
 * ``layers``    -- non-hot decoder arithmetic (delta rule, norms, rotary, attention)
 * ``target``    -- the verify forward of the whole target on the HIP kernels
+* ``quantized`` -- the quantized-weights seam (``OriginalQuantizedWeights`` interface)
+* ``session``   -- target session with a batched speculative verify
 * ``synthetic`` -- seeded synthetic workloads (tests and benchmark)
 * ``_lib``      -- ctypes binding of ``libdflash_hip.so``
 * ``build``     -- hipcc build recipe
 """
-from . import _lib, fused_ops, layers, ops, packing, plan, synthetic, target  # noqa: F401
+from . import _lib, fused_ops, layers, ops, packing, plan, quantized, session, synthetic, target  # noqa: F401
 from .packing import PackedW4, SharedExpert, concat_rows, pack_int4, quantize_w4  # noqa: F401
