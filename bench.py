@@ -297,6 +297,55 @@ def time_stack(pkg, device, steps, warmup, context=4096, tokens=16):
             "steps": steps, "graph_period": 4}
 
 
+def time_skewed(pkg, sets, device, top_k, steps, warmup, tokens=128, hot=16):
+    """The T=128 layer (8 verify blocks) with 16 hot experts taking ~50% of the assignments.
+
+    The bias b on the hot experts' logits is calibrated once on the first block's logits
+    (``synthetic.hot_expert_bias``); each step computes the router logits, adds the bias and
+    runs the layer on those logits (router, bias add and layer all timed).
+    """
+    gen = torch.Generator(device=device).manual_seed(128)
+    blocks = [torch.randn((tokens, 2048), device=device, generator=gen).to(torch.bfloat16) for _ in range(4)]
+    hot_ids = torch.randperm(256, generator=torch.Generator().manual_seed(7919))[:hot].to(device)
+    base = pkg.ops.router_logits(blocks[0], sets[0][3])
+    b = pkg.synthetic.hot_expert_bias(base, hot_ids, top_k)
+    bias = torch.zeros(256, device=device)
+    bias[hot_ids] = b
+    ws = torch.empty(pkg.ops.moe_workspace_bytes(tokens, 2048, 512, 256, top_k, 128, True), dtype=torch.uint8,
+                     device=device)
+    hits, hot_frac = [], []
+    for j in range(len(sets) * len(blocks)):
+        gu, dn, sh, router = sets[j % len(sets)]
+        lg = pkg.ops.router_logits(blocks[j % len(blocks)], router) + bias
+        _, r, _ = pkg.ops.moe_w4a16(blocks[j % len(blocks)], gu, dn, top_k=top_k, router_logits=lg, shared=sh,
+                                    workspace=ws, return_routing=True)
+        hits.append(int((r.offsets[1:] > r.offsets[:-1]).sum().item()))
+        hot_frac.append(float(torch.isin(r.ids.long(), hot_ids).float().mean().item()))
+
+    def step(j):
+        gu, dn, sh, router = sets[j % len(sets)]
+        x = blocks[j % len(blocks)]
+        pkg.ops.moe_w4a16(x, gu, dn, top_k=top_k, router_logits=pkg.ops.router_logits(x, router) + bias, shared=sh,
+                          workspace=ws)
+    ms = time_steps(step, steps, warmup)
+    hit = statistics.mean(hits)
+    int4 = (hit + 1) * INT4_BYTES_PER_EXPERT
+    gbs = int4 / (ms * 1e-3) / 1e9
+    return {"tokens": tokens, "hot_experts": hot, "bias": round(b, 4),
+            "hot_assignment_frac": round(statistics.mean(hot_frac), 3), "hit_experts_mean": round(hit, 1),
+            "us_per_layer": round(ms * 1e3, 2), "int4_bytes": int(int4), "int4_gbs": round(gbs, 1),
+            "hbm_frac_int4": round(gbs / HBM_PEAK_GBS, 4), "steps": steps,
+            "note": "router logits + bias add + layer per step, 3 rotated weight sets"}
+
+
+def measured_mfma():
+    """MFMA counters of the prefill gate/up tile kernel from the committed rocprofv3 passes, or None."""
+    path = ROOT / "profiles" / "mfma_prefill_t2048.json"
+    if not path.is_file():
+        return None
+    return json.loads(path.read_text())
+
+
 def measured_traffic():
     """HBM bytes per gate/up launch from the committed counter passes, or None."""
     path = ROOT / "profiles" / "hbm_traffic_gate_up_t16.json"
@@ -306,42 +355,79 @@ def measured_traffic():
     return int(round((rec["fetch_kib"] * rec["fetch_scale"] + rec["write_kib"] * rec["write_scale"]) * 1024))
 
 
-def cpu_baseline(pkg, tokens, top_k, seconds_budget=20.0):
-    """Oracle CPU restatement of the same layer (dense bf16 banks of the hit experts), median of timed runs."""
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_run(run, warmups=3, measured=10, budget_s=12.0):
+    """Median wall time of `measured` runs after `warmups` (fewer if the budget runs out, at least 3)."""
+    for _ in range(warmups):
+        run()
+    times, t_start = [], time.perf_counter()
+    for _ in range(measured):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget_s and len(times) >= 3:
+            break
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline(pkg, tokens, top_k):
+    """The oracle's CPU restatement of the same T=16 layer, shared expert included, on the host.
+
+    Protocol: 3 warmups + 10 timed runs, median; torch intra-op threads = every CPU this
+    process may run on.  ``value``: dense bf16 banks of the hit experts dequantised before the
+    timed region (the reference ``moe`` takes dense logical banks).  Also reported: the same
+    with every hit expert dequantised inside the timed call, and the single-qlinear workload
+    (``[16,2048] x [512,2048]``, dense and dequant-inclusive).
+    """
     import numpy as np
     from oracle import moe as oracle_moe, routing as oracle_routing, w4 as oracle_w4
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", min(16, os.cpu_count() or 1)))
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
     torch.set_num_threads(threads)
     layer = pkg.synthetic.moe_layer(tokens, seed=0)
     logits = oracle_moe.router_logits(layer.hidden, layer.router_weight)
     ids, _ = oracle_routing.topk(logits, top_k)
     hit = np.unique(ids).tolist()
-    e, i2, h = layer.gate_up.experts, layer.gate_up.rows, layer.gate_up.cols
-    # dense bf16 banks (the reference's input contract), dequantised outside the timed region;
-    # only hit experts are materialised, the others stay zero (never read)
-    gate_up = torch.zeros((e, i2, h), dtype=torch.bfloat16)
-    down = torch.zeros((e, h, i2 // 2), dtype=torch.bfloat16)
-    for ex in hit:
-        gate_up[ex] = torch.from_numpy(oracle_w4.dequantize(layer.gate_up.packed[ex].numpy(),
-                                                            layer.gate_up.scales[ex], 128)).to(torch.bfloat16)
-        down[ex] = torch.from_numpy(oracle_w4.dequantize(layer.down.packed[ex].numpy(),
-                                                         layer.down.scales[ex], 128)).to(torch.bfloat16)
-    run = lambda: oracle_moe.moe_dense(layer.hidden, logits, top_k, gate_up, down)  # noqa: E731
-    times = []
-    t_start = time.perf_counter()
-    for i in range(13):
-        t0 = time.perf_counter()
-        run()
-        if i >= 3:
-            times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > seconds_budget and len(times) >= 3:
-            break
-    med = statistics.median(times)
-    return {"value": round(med * 1e6, 1), "unit": "us/layer", "cores": threads, "kind": "port",
-            "sample": f"oracle.moe.moe_dense, T={tokens} routed experts (dense bf16 banks of the {len(hit)} hit "
-                      f"experts dequantised beforehand, shared expert not included), median of {len(times)} runs "
-                      f"after 3 warmups, torch CPU threads={threads}"}
+    gu, dn, sh = layer.gate_up, layer.down, layer.shared
+
+    def deq(bank, e=None):
+        return oracle_w4.dequantize_torch(bank.packed if e is None else bank.packed[e],
+                                          bank.scales if e is None else bank.scales[e], 128)
+    # dense bf16 banks, materialised for the hit experts only (the others are never read)
+    gate_up = torch.zeros((gu.experts, gu.rows, gu.cols), dtype=torch.bfloat16)
+    down = torch.zeros((dn.experts, dn.rows, dn.cols), dtype=torch.bfloat16)
+    for e in hit:
+        gate_up[e], down[e] = deq(gu, e), deq(dn, e)
+    shared_dense = (deq(sh.gate_up), deq(sh.down), sh.gate_weight)
+    dense_s, n_dense = _median_run(lambda: oracle_moe.moe_dense(layer.hidden, logits, top_k, gate_up, down,
+                                                                  shared=shared_dense))
+    fly_s, n_fly = _median_run(lambda: oracle_moe.moe_dense(
+        layer.hidden, logits, top_k, None, None, dequantize=lambda e: (deq(gu, e), deq(dn, e)),
+        shared=(deq(sh.gate_up), deq(sh.down), sh.gate_weight)))
+    # config 1: the single W4A16 qlinear
+    gen = torch.Generator().manual_seed(1)
+    x1 = torch.randn((16, 2048), generator=gen).to(torch.bfloat16)
+    w1 = pkg.synthetic.int4_weight(gen, (512, 2048), 128)
+    w1_dense = deq(w1)
+    ql_s, _ = _median_run(lambda: torch.nn.functional.linear(x1, w1_dense), warmups=3, measured=10)
+    ql_fly_s, _ = _median_run(lambda: torch.nn.functional.linear(x1, deq(w1)), warmups=3, measured=10)
+    return {"value": round(dense_s * 1e6, 1), "unit": "us/layer", "cores": threads, "kind": "port",
+            "cpu_model": _cpu_model(), "cpu_count": os.cpu_count(),
+            "sample": f"oracle.moe.moe_dense: the T={tokens} layer (router logits given, top-{top_k} over 256 "
+                      f"experts, {len(hit)} hit experts + the gated shared expert, fp32 combine) on dense bf16 "
+                      f"banks dequantised before timing; median of {n_dense} runs after 3 warmups, "
+                      f"torch threads={threads}",
+            "dequant_inclusive_us": round(fly_s * 1e6, 1), "dequant_inclusive_runs": n_fly,
+            "qlinear_config1_us": round(ql_s * 1e6, 1), "qlinear_config1_dequant_inclusive_us": round(ql_fly_s * 1e6, 1)}
 
 
 def main() -> int:
@@ -354,6 +440,7 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-qlinear", action="store_true")
     ap.add_argument("--no-stack", action="store_true")
+    ap.add_argument("--no-config3", action="store_true")
     ap.add_argument("--only-stack", action="store_true", help="time the 40-layer stack only (no JSON metric line)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (reference dispatch for HBM byte counters)")
@@ -431,8 +518,23 @@ def main() -> int:
         steps_p = max(5, args.steps // 10)
         ms_p = time_layer(pkg, sets, blocks_p, top_k, steps_p, max(2, args.warmup // 10), ws)
         tflops = moe_flops(2048, top_k) / (ms_p * 1e-3) / 1e12
-        result["prefill"] = {"tokens": 2048, "us_per_layer": round(ms_p * 1e3, 1), "tflops": round(tflops, 2),
-                             "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4), "steps": steps_p}
+        gu_p_ms, _ = time_stage(pkg, sets, blocks_p, top_k, steps_p, max(2, args.warmup // 10))
+        dn_p_ms, _ = time_stage(pkg, sets, blocks_p, top_k, steps_p, max(2, args.warmup // 10), pkg.ops.STAGE_DOWN)
+        gu_flops = 2 * (2048 * top_k + 2048) * 1024 * 2048
+        gu_tf = gu_flops / (gu_p_ms * 1e-3) / 1e12
+        result["prefill"] = {
+            "tokens": 2048, "us_per_layer": round(ms_p * 1e3, 1), "tflops": round(tflops, 2),
+            "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4), "steps": steps_p,
+            "roofline": {"bound": "mfma", "achieved": round(gu_tf, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(gu_tf / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                         "kernel": "w4_tile_kernel<1, unsigned short> (grouped gate/up + SiLU*up, T=2048, tiled)",
+                         "kernel_us": round(gu_p_ms * 1e3, 2), "flops_per_launch": gu_flops,
+                         "counters": measured_mfma()},
+            "down_kernel_us": round(dn_p_ms * 1e3, 2),
+            "down_kernel_tflops": round(2 * (2048 * top_k + 2048) * 2048 * 512 / (dn_p_ms * 1e-3) / 1e12, 1)}
+    if not args.no_config3:
+        log("timing the T=128 skewed layer")
+        result["skewed_t128"] = time_skewed(pkg, sets, device, top_k, max(24, args.steps // 2), args.warmup)
     if not args.no_stack:
         log("timing the 40-layer verify stack")
         result["stack"] = time_stack(pkg, device, max(8, args.steps // 10), max(4, args.warmup // 5))

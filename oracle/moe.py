@@ -98,22 +98,34 @@ def moe(hidden: torch.Tensor, logits: np.ndarray, top_k: int, gate_up, down, gro
                 out_f32=out, out=out.to(torch.bfloat16))
 
 
-def moe_dense(hidden: torch.Tensor, logits: np.ndarray, top_k: int, gate_up: torch.Tensor,
-              down: torch.Tensor) -> torch.Tensor:
-    """Same routed MoE over pre-dequantised dense banks ``[E,2I,H]`` / ``[E,H,I]`` (any float dtype).
+def moe_dense(hidden: torch.Tensor, logits: np.ndarray, top_k: int, gate_up, down, *, shared=None,
+              dequantize=None) -> torch.Tensor:
+    """Same routed MoE over dense banks ``[E,2I,H]`` / ``[E,H,I]`` (any float dtype).
 
     This is the CPU-baseline form: the reference's ``moe`` consumes dense
     logical banks (``reference/fused_ops.py:148-159``).  Math runs in the
-    banks' dtype per expert, combine in float32.
+    banks' dtype per expert, combine in float32.  ``shared`` = (gate_up
+    ``[2I,H]``, down ``[H,I]``, gate vector ``[H]``) adds the gated shared expert
+    (``fused/model.py:305-307``).  With ``dequantize`` (a function of an expert
+    index returning its dense ``(gate_up, down)``), ``gate_up``/``down`` are
+    ignored and each hit expert is dequantised inside the call.
     """
-    x = hidden.reshape(-1, hidden.shape[-1]).to(gate_up.dtype)
+    dtype = gate_up.dtype if dequantize is None else torch.bfloat16
+    x = hidden.reshape(-1, hidden.shape[-1]).to(dtype)
     ids, weights = routing.topk(np.asarray(logits, dtype=np.float32), top_k)
     routed = torch.zeros((x.shape[0], top_k, x.shape[1]), dtype=torch.float32)
     for expert in np.unique(ids).tolist():
         rows, slots = np.nonzero(ids == expert)
-        gate, up = F.linear(x[rows], gate_up[expert]).chunk(2, dim=-1)
-        routed[rows, slots] = F.linear(F.silu(gate) * up, down[expert]).to(torch.float32)
-    return (routed * torch.from_numpy(weights)[..., None]).sum(dim=1).to(hidden.dtype)
+        gu, dn = (gate_up[expert], down[expert]) if dequantize is None else dequantize(expert)
+        gate, up = F.linear(x[rows], gu).chunk(2, dim=-1)
+        routed[rows, slots] = F.linear(F.silu(gate) * up, dn).to(torch.float32)
+    out = (routed * torch.from_numpy(weights)[..., None]).sum(dim=1)
+    if shared is not None:
+        sgu, sdn, sgate = shared
+        gate, up = F.linear(x, sgu).chunk(2, dim=-1)
+        y = F.linear(F.silu(gate) * up, sdn).to(torch.float32)
+        out = out + y * torch.sigmoid(x.to(torch.float32) @ sgate.to(torch.float32))[:, None]
+    return out.to(hidden.dtype)
 
 
 def moe_reference_order(hidden: torch.Tensor, logits: np.ndarray, top_k: int, gate_up: torch.Tensor,

@@ -94,6 +94,18 @@ def dequantize(packed, scales, group_size: int) -> np.ndarray:
     return q * np.repeat(s, group_size, axis=-1)
 
 
+def dequantize_torch(packed: torch.Tensor, scales: torch.Tensor, group_size: int,
+                     dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """``dequantize`` with torch CPU ops (multi-threaded), rounded to ``dtype``: the form the CPU
+    baseline times when it dequantises experts on the fly.  Equal to ``dequantize`` in float32."""
+    low = (packed & 15).to(torch.int8)
+    high = (packed >> 4).to(torch.int8)
+    q = torch.stack((low, high), dim=-1).reshape(*packed.shape[:-1], packed.shape[-1] * 2)
+    q = torch.where(q >= 8, q - 16, q).to(torch.float32)
+    s = scales.to(torch.float32).repeat_interleave(group_size, dim=-1)
+    return (q * s).to(dtype)
+
+
 def qlinear(x: torch.Tensor, packed, scales, group_size: int, *, accumulate: str = "fp64") -> np.ndarray:
     """W4A16 linear ``y[m, n] = sum_k x[m, k] * q[n, k] * s[n, k // G]`` as float64/float32.
 

@@ -124,6 +124,27 @@ def test_dense_baseline_form_matches():
     assert metrics.compare(dense, golden)["max_rel"] < 1e-2
 
 
+def test_dense_baseline_with_shared_expert_and_on_the_fly_dequant():
+    """The CPU baseline's two timed forms (pre-dequantised bf16 banks; hit experts dequantised
+    inside the call) both give the golden layer, shared expert included."""
+    x, logits, gu, dn = _random_layer(8)
+    gen = torch.Generator().manual_seed(9)
+    sgu = (torch.randint(0, 256, (256, 128), dtype=torch.uint8, generator=gen),
+           (torch.rand((256, 2), generator=gen) * 0.015 + 0.005).to(torch.bfloat16))
+    sdn = (torch.randint(0, 256, (256, 64), dtype=torch.uint8, generator=gen),
+           (torch.rand((256, 1), generator=gen) * 0.015 + 0.005).to(torch.bfloat16))
+    sgate = (torch.randn(256, generator=gen) * 0.02).to(torch.bfloat16)
+    golden = moe.moe(x, logits, 2, gu, dn, 128, shared=(sgu, sdn, sgate))["out_f32"]
+    dense_shared = (w4.dequantize_torch(*sgu, 128), w4.dequantize_torch(*sdn, 128), sgate)
+    pre = moe.moe_dense(x, logits, 2, _deq(gu, 128).to(torch.bfloat16), _deq(dn, 128).to(torch.bfloat16),
+                        shared=dense_shared)
+    fly = moe.moe_dense(x, logits, 2, None, None, shared=dense_shared,
+                        dequantize=lambda e: (w4.dequantize_torch(gu[0][e], gu[1][e], 128),
+                                              w4.dequantize_torch(dn[0][e], dn[1][e], 128)))
+    assert torch.equal(pre, fly)
+    assert metrics.compare(pre, golden)["max_rel"] < 2e-2
+
+
 def test_metrics_definitions():
     a = np.array([1.0, -2.0, 3.0])
     r = metrics.compare(a, a)

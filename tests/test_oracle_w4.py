@@ -159,3 +159,13 @@ def test_from_int8_rejects_what_the_reader_rejects(case):
     with pytest.raises(ValueError, match=match):
         w4.from_int8(values, scales, tiled=False)
 
+
+
+def test_dequantize_torch_equals_dequantize():
+    """The CPU baseline's vectorised dequantiser equals the oracle's, every byte value included."""
+    gen = torch.Generator().manual_seed(17)
+    packed = torch.randint(0, 256, (3, 32, 256), dtype=torch.uint8, generator=gen)
+    packed[0, 0, :] = torch.arange(256, dtype=torch.uint8)
+    scales = (torch.rand((3, 32, 4), generator=gen) * 0.015 + 0.005).to(torch.bfloat16)
+    got = w4.dequantize_torch(packed, scales, 128, torch.float32)
+    np.testing.assert_array_equal(got.numpy(), w4.dequantize(packed.numpy(), scales, 128))
