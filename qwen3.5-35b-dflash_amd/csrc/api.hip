@@ -170,10 +170,9 @@ int cu_count() {
 
 int token_tiles(int64_t T) { return T <= 16 ? 1 : 2; }
 
-// The verify kernels take blocks of at most 32 tokens and 2048 routed slot rows;
-// other small blocks use passes of 16 * token_tiles(T) rows on the streaming kernel.
+// Blocks of up to 32 tokens keep all their x rows in the verify gate/up launch's LDS (and
+// may route inside it); larger ones stage x rows per chunk of passes, gathered by token.
 constexpr int64_t kVerifyMaxTokens = 32;
-constexpr int64_t kVerifyMaxTokenRows = 2048;
 
 int check_route_args(int64_t T, int64_t E, int64_t k) {
   if (T < 0) return fail(DFLASH_ERR_INVALID_ARGUMENT, "tokens must be >= 0");
@@ -299,7 +298,9 @@ bool w4_path_reads_tiled(int mode, int N, int K, int G, GemmPath path) {
 bool verify_fits(const MoeShapes& S, bool route, dflash::VerifyParams* gu, dflash::VerifyParams* dn) {
   using namespace dflash;
   const auto group_ok = [](int64_t g) { return g == 128 || g == 256; };
-  if (S.T > kVerifyMaxTokens || S.T * S.k > kVerifyMaxTokenRows || !group_ok(S.G) || !group_ok(S.Gd)) return false;
+  if (!group_ok(S.G) || !group_ok(S.Gd)) return false;
+  // long prefill (at least 16 rows per expert on average) belongs to the MFMA tile kernel
+  if (S.T > kVerifyMaxTokens && moe_tile_path(S)) return false;
   const int T = static_cast<int>(S.T), H = static_cast<int>(S.H), I = static_cast<int>(S.I);
   const int E = static_cast<int>(S.E), k = static_cast<int>(S.k), sh = S.shared ? 1 : 0;
   *gu = VerifyParams{};
@@ -831,7 +832,7 @@ static int moe_w4a16_body(const void* hidden, int64_t tokens, int64_t hidden_siz
     const bool small = dflash::route_small_fits(T, E, static_cast<int>(S.k));
     // the verify path routes inside its gate/up launch when the block fits there
     dflash::VerifyParams vgu{}, vdn{};
-    const bool verify = tokens > 0 && small && verify_fits(S, true, &vgu, &vdn);
+    const bool verify = tokens > 0 && verify_fits(S, small, &vgu, &vdn);
     if (int r = check_tiled_moe(S, verify)) return r;
     float* logits = router_logits ? const_cast<float*>(router_logits)
                                   : (logits_out ? logits_out : at<float>(workspace, L.logits));

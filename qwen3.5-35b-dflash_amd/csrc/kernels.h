@@ -172,7 +172,8 @@ struct VerifyParams {
   int lds_a, lds_neg, lds_tok, lds_pdesc, lds_wgt, lds_part, lds_scratch, lds_bytes;  // lds_wgt: down's raw partials
   int pd_cap;        // pass descriptors the LDS holds
   int a_rows;        // activation rows the LDS holds (gate/up: T; linear: M; down: chunk_passes * 16)
-  int chunk_passes;  // down: passes whose h rows are staged at once
+  int chunk_passes;  // down (and gathered gate/up): passes whose activation rows are staged at once
+  int gather;        // gate/up: stage per chunk only its passes' x rows, gathered by token (any T)
   // in-kernel routing (gate/up only; 1: one wave per token, 2: one 16-lane row per token):
   // fp32 logits [T][E] -> the dflash_moe_route outputs (written by workgroup 0) and the
   // work table of the down launch

@@ -650,7 +650,8 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
                      __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w));
   };
 
-  const int chunk_passes = kMode == kModeDown ? vp.chunk_passes : max(P_last - P_first + 1, 1);
+  const bool chunked = kMode == kModeDown || (kMode == kModeGateUp && vp.gather);
+  const int chunk_passes = chunked ? vp.chunk_passes : max(P_last - P_first + 1, 1);
   for (int Pc = P_first; Pc <= P_last; Pc += chunk_passes) {
     const int Pc_end = min(P_last + 1, Pc + chunk_passes);
     const int cb = max(ub, Pc * strips), ce = min(ue, Pc_end * strips);
@@ -744,7 +745,35 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
       for (int i = 0; i + 1 < kVDepth; ++i) issue(wbuf[i], sbuf[i]);
 
       // ---- stage the chunk's activation rows and descriptors
-      if (kMode == kModeGateUp || kMode == kModeLinear) {
+      if (kMode == kModeGateUp && vp.gather) {
+        // the chunk's pass descriptors; per pass its 16 slot rows' x rows (the token of a
+        // routed row from the work table, clamped to the slot like the compute indexes) and
+        // their -136*sum terms, all by direct-to-LDS loads
+        pd_base = Pc;
+        const int npass = Pc_end - Pc;
+        const buf_rsrc tr = make_rsrc(p.pass_table, static_cast<uint32_t>(total_passes) * 16);
+        if (wave == 0)
+          dma16(tr, lds_pdesc, static_cast<uint32_t>(min(Pc + lane, total_passes - 1) * 16), 0);
+        const buf_rsrc xr = make_rsrc(p.act, static_cast<uint32_t>(p.T) * kK * 2);
+        constexpr int kBlk = kK / 512;
+        for (int i = wave; i < npass * 16 * kBlk; i += kVWaves) {
+          const int rr = i / kBlk, bl = i - rr * kBlk;
+          const int4 d = early_desc(Pc + rr / 16);
+          const int m = min(d.w + (rr & 15), d.z - 1);
+          const int t = d.x < 0 ? m : ld_const(p.tok, d.y + m);
+          dma16(xr, lds_a + rr * kRS + bl * 1024, static_cast<uint32_t>(lane * 16),
+                static_cast<uint32_t>((t * kK + bl * 512) * 2));
+        }
+        // 64 terms per load: 64 / kNKB rows, all of one pass (kNKB divides 16 * kNKB)
+        const buf_rsrc nr = make_rsrc(p.act_neg, static_cast<uint32_t>(p.T) * kNKB * 4);
+        for (int i = wave; i * 64 < npass * 16 * kNKB; i += kVWaves) {
+          const int4 d = early_desc(Pc + (i * 64) / (16 * kNKB));
+          const int f = 64 * i + lane, rr = f / kNKB, kb = f - rr * kNKB;
+          const int m = min(d.w + (rr & 15), d.z - 1);
+          const int t = d.x < 0 ? m : p.tok[d.y + m];
+          dma4(nr, lds_neg + 64 * i, static_cast<uint32_t>((t * kNKB + kb) * 4), 0);
+        }
+      } else if (kMode == kModeGateUp || kMode == kModeLinear) {
         if (!(kMode == kModeGateUp && vp.route)) {
           // the token of every slot row and the chunk's pass descriptors (in-kernel routing
           // left both in LDS and staged x already)
@@ -822,17 +851,17 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
               const int M = cd.z, m0 = cd.w;
               const int ma = min(m0 + lr, M - 1);
               int arow;
-              if (kMode == kModeGateUp) arow = cd.x < 0 ? ma : lds_tok[cd.y + ma];
-              else if (kMode == kModeLinear) arow = ma;
-              else arow = (P - Pc) * 16 + lr;
+              if (chunked) arow = (P - Pc) * 16 + lr;
+              else if (kMode == kModeGateUp) arow = cd.x < 0 ? ma : lds_tok[cd.y + ma];
+              else arow = ma;
               a_off = arow * kRS + kq * 64;
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
                 const int me = min(m0 + 4 * kq + e, M - 1);
                 int nrow;
-                if (kMode == kModeGateUp) nrow = cd.x < 0 ? me : lds_tok[cd.y + me];
-                else if (kMode == kModeLinear) nrow = me;
-                else nrow = (P - Pc) * 16 + 4 * kq + e;
+                if (chunked) nrow = (P - Pc) * 16 + 4 * kq + e;
+                else if (kMode == kModeGateUp) nrow = cd.x < 0 ? me : lds_tok[cd.y + me];
+                else nrow = me;
                 n_idx[e] = nrow * kNKB;
               }
               began = kb == 0;
@@ -913,7 +942,8 @@ __global__ __launch_bounds__(512) void w4_verify_kernel(VerifyParams vp) {
 bool verify_layout(int mode, int T, int K, int N, int E, int k, int has_shared, int route, VerifyParams* vp) {
   // K = 4096 (the attention output projections) only as a plain linear: its x rows fill most of the LDS
   if (K != 512 && K != 1024 && K != 2048 && !(K == 4096 && mode == kModeLinear)) return false;
-  if (T <= 0 || T > 32 || k <= 0) return false;
+  // gate/up and down stage per chunk of passes when needed, so only linear mode bounds T
+  if (T <= 0 || (mode == kModeLinear && T > 32) || k <= 0) return false;
   if (N % (mode == kModeGateUp ? 32 : kVStrip)) return false;
   const int rs = 2 * K + 16, nkb = K / 128;
   auto al = [](int v) { return (v + 15) & ~15; };
@@ -926,6 +956,30 @@ bool verify_layout(int mode, int T, int K, int N, int E, int k, int has_shared, 
   };
   VerifyParams& L = *vp;
   L.route = 0;
+  L.gather = 0;
+  // gathered gate/up (blocks above 32 tokens, or whose whole-block plan below does not fit):
+  // per chunk of passes, 16 x rows each (by token) and their -136*sum terms, like down's h rows
+  auto gather_layout = [&]() {
+    off = 0;
+    const int per_pass = 16 * rs + al(16 * nkb * 4);
+    const int fixed = part + 64 * 16;
+    const int cp = std::min(8, (kVLds - fixed) / per_pass);
+    if (cp < 1) return false;
+    L.route = 0;
+    L.gather = 1;
+    L.chunk_passes = cp;
+    L.pd_cap = 64;
+    L.a_rows = cp * 16;
+    L.lds_a = take(cp * 16 * rs);
+    L.lds_neg = take(cp * 16 * nkb * 4);
+    L.lds_wgt = 0;
+    L.lds_pdesc = take(64 * 16);
+    L.lds_tok = 0;
+    L.lds_part = L.lds_scratch = take(part);
+    L.lds_bytes = off;
+    return off <= kVLds;
+  };
+  if (mode == kModeGateUp && T > 32) return gather_layout();
   if (mode == kModeDown) {
     // per pass: 16 h rows, their -136*sum terms and raw partials (8 per k-block)
     const int per_pass = 16 * rs + al(16 * nkb * 4) + al(16 * nkb * 8 * 4);
@@ -976,7 +1030,8 @@ bool verify_layout(int mode, int T, int K, int N, int E, int k, int has_shared, 
     L.lds_part = L.lds_scratch = take(part);
   }
   L.lds_bytes = off;
-  return off <= kVLds;
+  if (off <= kVLds) return true;
+  return mode == kModeGateUp && gather_layout();  // whole-block plan too large: gathered chunks
 }
 
 
