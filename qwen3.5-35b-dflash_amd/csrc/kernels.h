@@ -137,7 +137,7 @@ void launch_from_int8(const int8_t* values, const void* scales, int scales_dtype
                       hipStream_t stream);
 
 void launch_front(const FrontParams& p, hipStream_t stream);
-// Router tiles of a launch: 32 tokens x 64 experts when T >= 64 and H % 128 == 0, else 16 x 16.
+// Router tiles of a launch: 32 tokens x 64 experts when T >= 1024 and H in {512, 1024, 2048}, else 16 x 16.
 bool router_big_fits(int T, int H);
 int router_tiles(int T, int E, int H);
 bool route_small_fits(int T, int E, int k);

@@ -286,16 +286,43 @@ __global__ __launch_bounds__(1024) void route_small_kernel(RouteParams p) {
   for (int i = tid; i < kMaxExperts; i += 1024) counts[i] = 0;
   for (int i = tid; i < (E * tpad) / 4; i += 1024) slotmap_words[i] = 0u;
   __syncthreads();
-  for (int t = wave; t < T; t += 16) {
-    int id;
-    float w;
-    topk_any(p.logits + static_cast<int64_t>(t) * E, E, k, &id, &w);
+  auto record = [&](int t, int id, float w) {
     if (lane < k) {
       p.ids[t * k + lane] = id;
       p.wts[t * k + lane] = w;
       wts_lds[t * k + lane] = w;
       atomicAdd(&counts[id], 1);
       slotmap[id * tpad + t] = static_cast<uint8_t>(lane + 1);
+    }
+  };
+  if (E <= 256) {
+    // tokens wave, wave + 16, ... in groups of 4: the group's logit rows are all requested
+    // before the first selection, so a wave waits for one memory round trip per group
+    constexpr int kGroup = 4;
+    for (int t0 = wave; t0 < T; t0 += 16 * kGroup) {
+      uint32_t key[kGroup][4];
+#pragma unroll
+      for (int g = 0; g < kGroup; ++g) {
+        const int t = min(t0 + 16 * g, T - 1);  // past the end: reload the last row, not recorded
+        load_keys<4>(p.logits + static_cast<int64_t>(t) * E, E, key[g]);
+      }
+#pragma unroll
+      for (int g = 0; g < kGroup; ++g) {
+        const int t = t0 + 16 * g;
+        if (t < T) {
+          int id;
+          float w;
+          select_keys<4>(key[g], k, &id, &w);
+          record(t, id, w);
+        }
+      }
+    }
+  } else {
+    for (int t = wave; t < T; t += 16) {
+      int id;
+      float w;
+      topk_any(p.logits + static_cast<int64_t>(t) * E, E, k, &id, &w);
+      record(t, id, w);
     }
   }
   __syncthreads();
@@ -642,7 +669,10 @@ __global__ __launch_bounds__(64) void combine_kernel(const YT* __restrict__ y, c
 
 // ---------------------------------------------------------------------------
 // host launchers
-bool router_big_fits(int T, int H) { return T >= 64 && (H == 512 || H == 1024 || H == 2048); }
+// 32 x 64 tiles read 384 KB each: they pay only with enough of them to fill the CUs (T=2048 at
+// E=256 gives 256); below, 16 x 16 tiles spread the router rows over more workgroups
+// (T=128: 128 tiles of 64 KB instead of 16 of 384 KB).
+bool router_big_fits(int T, int H) { return T >= 1024 && (H == 512 || H == 1024 || H == 2048); }
 
 int router_tiles(int T, int E, int H) {
   return router_big_fits(T, H) ? ((T + 31) / 32) * ((E + 63) / 64) : ((T + 15) / 16) * ((E + 15) / 16);
@@ -655,8 +685,11 @@ void launch_front(const FrontParams& p, hipStream_t stream) {
   hipLaunchKernelGGL(front_kernel, dim3(blocks), dim3(512), 0, stream, p);
 }
 
+// One workgroup selects 16 tokens at a time: above 32 tokens the per-token waves of the
+// multi-workgroup kernels finish sooner (T=128: 40 us in one workgroup).
 bool route_small_fits(int T, int E, int k) {
-  return static_cast<int64_t>(T) * k <= kSmallPairs && static_cast<int64_t>((T + 3) & ~3) * E <= kSmallSlotBytes;
+  return T <= 32 && static_cast<int64_t>(T) * k <= kSmallPairs &&
+         static_cast<int64_t>((T + 3) & ~3) * E <= kSmallSlotBytes;
 }
 
 int64_t route_zero_words(int T, int E) {

@@ -42,14 +42,19 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 // first non-empty block): the larger logit wins and, among equal logits, the
 // lower expert id.  Lane s < k ends with (id_s, weight_s).
 template <int kPer>
-__device__ __forceinline__ void wave_topk(const float* __restrict__ row, int E, int k, int* id_out, float* w_out) {
+__device__ __forceinline__ void load_keys(const float* __restrict__ row, int E, uint32_t (&key)[kPer]) {
   const int lane = lane_id();
-  uint32_t key[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int e = lane + 64 * i;
     key[i] = e < E ? sortable_key(row[e]) + 1u : 0u;  // sortable keys stay below 0xFF800001
   }
+}
+
+// The k selection rounds and the weights of wave_topk over keys already loaded (load_keys).
+template <int kPer>
+__device__ __forceinline__ void select_keys(uint32_t (&key)[kPer], int k, int* id_out, float* w_out) {
+  const int lane = lane_id();
   int my_id = -1;
   uint32_t my_key = 0;
   for (int s = 0; s < k; ++s) {
@@ -77,6 +82,13 @@ __device__ __forceinline__ void wave_topk(const float* __restrict__ row, int E, 
   const float total = wave_sum(ex);
   *id_out = my_id;
   *w_out = ex / total;
+}
+
+template <int kPer>
+__device__ __forceinline__ void wave_topk(const float* __restrict__ row, int E, int k, int* id_out, float* w_out) {
+  uint32_t key[kPer];
+  load_keys<kPer>(row, E, key);
+  select_keys<kPer>(key, k, id_out, w_out);
 }
 
 __device__ __forceinline__ void topk_any(const float* row, int E, int k, int* id, float* w) {
