@@ -205,6 +205,7 @@ def time_experts(pkg, sets, blocks, top_k, steps, warmup, workspace):
 
 
 GATE_UP_BYTES_PER_EXPERT = 2 * 512 * 2048 // 2 + 2 * 512 * (2048 // 128) * 2   # int4 + bf16 scales
+DOWN_BYTES_PER_EXPERT = 2048 * 512 // 2 + 2048 * (512 // 128) * 2
 
 
 def time_stage(pkg, sets, blocks, top_k, steps, warmup, stage=None, given_logits=False):
@@ -347,7 +348,7 @@ def measured_mfma():
 
 
 def measured_traffic():
-    """HBM bytes per gate/up launch from the committed counter passes, or None."""
+    """HBM bytes per T=16 gate/up launch from the committed counter passes, or None."""
     path = ROOT / "profiles" / "hbm_traffic_gate_up_t16.json"
     if not path.is_file():
         return None
@@ -480,13 +481,26 @@ def main() -> int:
     int4_bytes = (hits + 1) * INT4_BYTES_PER_EXPERT
     all_bytes = (hits + 1) * (INT4_BYTES_PER_EXPERT + SCALE_BYTES_PER_EXPERT)
     layer_gbs = int4_bytes / (ms * 1e-3) / 1e9
-    log("timing the gate/up kernel with HIP events")
+    log("timing the expert kernels with HIP events")
+    # gate/up and down as separate launches (the default), and as one launch (opt-in)
+    lay_ms, lay_hits = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup, pkg.ops.STAGE_EXPERTS,
+                                  given_logits=True)
+    pkg.ops.set_fused_layer(True)
+    try:
+        fused_ms, _ = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup, pkg.ops.STAGE_EXPERTS,
+                                 given_logits=True)
+        fused_layer_ms = time_layer(pkg, sets, blocks, top_k, args.steps, args.warmup, ws)
+    finally:
+        pkg.ops.set_fused_layer(False)
     gu_ms, gu_hits = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup, given_logits=True)
     stream_ms, _ = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup)
     dn_ms, _ = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup, pkg.ops.STAGE_DOWN)
-    # algorithmic bytes of one gate/up launch: the hit experts' and the shared
-    # expert's int4 gate/up rows + bf16 scales, x read, h (bf16) written
-    gu_bytes = (gu_hits + 1) * GATE_UP_BYTES_PER_EXPERT + tokens * 2048 * 2 + (tokens * top_k + tokens) * 512 * 2
+    # algorithmic bytes of one gate/up launch: the hit experts' and the shared expert's int4
+    # gate/up rows + bf16 scales, x (bf16) read, h (bf16) written; of both expert launches:
+    # gate/up and down rows + scales, x read, the fp32 y rows the combine reads written
+    rows = tokens * top_k + tokens
+    gu_bytes = (gu_hits + 1) * GATE_UP_BYTES_PER_EXPERT + tokens * 2048 * 2 + rows * 512 * 2
+    lay_bytes = (lay_hits + 1) * (GATE_UP_BYTES_PER_EXPERT + DOWN_BYTES_PER_EXPERT) + tokens * 2048 * 2 + rows * 2048 * 4
     achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
 
     result = {
@@ -509,6 +523,10 @@ def main() -> int:
                      "bytes_per_launch": int(gu_bytes)},
         "stages": {"expert_stage_us": round(exp_ms * 1e3, 2), "down_kernel_us": round(dn_ms * 1e3, 2),
                    "gate_up_stream_only_us": round(stream_ms * 1e3, 2),
+                   "expert_kernels_us": round(lay_ms * 1e3, 2),
+                   "expert_kernels_gbs": round(lay_bytes / (lay_ms * 1e-3) / 1e9, 1),
+                   "one_launch_expert_kernel_us": round(fused_ms * 1e3, 2),
+                   "one_launch_layer_us": round(fused_layer_ms * 1e3, 2),
                    "expert_int4_bytes": int(int4_bytes), "expert_weight_bytes": int(all_bytes),
                    "expert_stage_int4_gbs": round(int4_bytes / (exp_ms * 1e-3) / 1e9, 1)},
     }

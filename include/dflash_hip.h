@@ -175,6 +175,23 @@ int dflash_moe_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, co
                      void* stream);
 
 /*
+ * One-launch expert FFN (no counterpart in the reference).  When enabled (process-wide,
+ * off by default), a verify block (T <= 32) that dflash_moe_w4a16 routes inside its gate/up
+ * launch, with one scale dtype for both banks, on a device of 8 XCDs, runs gate/up and down
+ * as one launch: pass P belongs to XCD P % 8, whose workgroups (as the hardware placed
+ * them) claim its gate/up, then its down ranges and hand h rows to each other in that XCD's
+ * L2.  Same results as the two launches up to the order of fp32 sums inside a tile.
+ * dflash_moe_fused_status_offset returns the byte offset in the workspace of that launch's
+ * status word, cleared by every call: after the call it holds bit 0 when a workgroup read
+ * an XCD id above 7 and bit 1 when a wait for gate/up rows gave up (the output is then
+ * wrong); -1 when a layer of this shape runs the separate launches.  It needs the current
+ * device (its CU and XCD counts).
+ */
+int dflash_set_fused_layer(int enable);
+int64_t dflash_moe_fused_status_offset(int64_t tokens, int64_t hidden_size, int64_t inter_size, int64_t experts,
+                                       int64_t top_k, int64_t group_size, int has_shared);
+
+/*
  * dflash_moe_w4a16 without a workspace: the same layer, arguments and results, with its
  * scratch in a static device array of DFLASH_NOALLOC_SCRATCH_BYTES (8 MiB) that each GPU
  * the library runs on holds until the process ends.  No counterpart in the reference: it
@@ -202,12 +219,19 @@ int dflash_moe_w4a16_noalloc(const void* hidden, int64_t tokens, int64_t hidden_
  * output again (out is not written).  On the verify path (T <= 32) the gate/up
  * kernel also routes the block in its prologue; in measurement mode it does so
  * only when the call passes router_logits (else it reads the work table).
+ * Where dflash_moe_w4a16 runs gate/up and down as one launch (T <= 32, the block
+ * routed in that launch), DFLASH_STAGE_EXPERTS with router_logits relaunches
+ * that kernel; GATE_UP and DOWN alone, or EXPERTS without router_logits, run
+ * the two separate verify kernels of the same layer instead (their intermediate
+ * rows can differ from the one launch's in the last bit: the two split a tile's
+ * k-blocks over waves differently).
  * DFLASH_STAGE_NONE restores full calls.  Process-wide.
  */
 enum dflash_stage {
   DFLASH_STAGE_NONE = 0,
   DFLASH_STAGE_GATE_UP = 1, /* grouped gate/up GEMM + SiLU*up of the expert FFN */
-  DFLASH_STAGE_DOWN = 2     /* grouped down GEMM of the expert FFN */
+  DFLASH_STAGE_DOWN = 2,    /* grouped down GEMM of the expert FFN */
+  DFLASH_STAGE_EXPERTS = 3  /* every expert GEMM kernel of the call (gate/up and down) */
 };
 int dflash_set_measure_stage(int stage);
 

@@ -67,12 +67,15 @@ SIGNATURES = {
                                         _P, _P, _P, _P, _SZ, _P]),
     "dflash_moe_w4a16_noalloc": (ctypes.c_int, [_P, _I64, _I64, _P, _P, _I64, _W4P, _W4P, _W4P, _W4P, _P, _P, _P, _P,
                                                 _P, _P, _P, _P, _P]),
+    "dflash_set_fused_layer": (ctypes.c_int, [ctypes.c_int]),
+    "dflash_moe_fused_status_offset": (_I64, [_I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_int]),
     "dflash_set_measure_stage": (ctypes.c_int, [ctypes.c_int]),
 }
 
 STAGE_NONE = 0
 STAGE_GATE_UP = 1
 STAGE_DOWN = 2
+STAGE_EXPERTS = 3
 
 
 class DflashError(RuntimeError):

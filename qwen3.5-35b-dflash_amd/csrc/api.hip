@@ -101,6 +101,11 @@ constexpr int kDownPlanMaxGrid = 1024;
 struct MoeLayout {
   RouteLayout route;
   size_t logits, x_il, xneg, gate, h, hpart, y, down_plan, total;
+  // fused layer launch: per XCD a block of ready_stride words (its per-pass counts, then its
+  // two queues), then the done count and the error word on lines of their own; ready_words
+  // covers them all (the front launch clears them)
+  size_t ready, done, err, ready_words;
+  int ready_stride;
 };
 
 MoeLayout moe_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, bool shared) {
@@ -117,6 +122,14 @@ MoeLayout moe_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, bool
   L.hpart = c.take(4 * rows * (I / 16));
   L.y = c.take(4 * rows * H);
   L.down_plan = c.take(48 * static_cast<size_t>(kDownPlanMaxGrid));
+  // a pass holds at least one row: at most T*k + T passes, ceil of an eighth per XCD; each
+  // XCD's block (counts + 2 queues) rounded up to 128-byte lines
+  const int64_t local = (T * k + T + dflash::kXcds - 1) / dflash::kXcds;
+  L.ready_stride = static_cast<int>(std::min<int64_t>((local + 2 + 31) / 32 * 32, int64_t(1) << 28));
+  L.ready_words = static_cast<size_t>(dflash::kXcds) * L.ready_stride + 64;
+  L.ready = c.take(4 * L.ready_words);
+  L.done = L.ready + 4 * static_cast<size_t>(dflash::kXcds) * L.ready_stride;
+  L.err = L.done + 128;
   L.total = c.off;
   return L;
 }
@@ -164,6 +177,18 @@ int cu_count() {
   int n = cache[dev].load(std::memory_order_relaxed);
   if (n > 0) return n;
   if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+  cache[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+// XCDs (XCCs) of the current device, 0 when unknown.
+int xcc_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || n <= 0) return 0;
   cache[dev].store(n, std::memory_order_relaxed);
   return n;
 }
@@ -255,9 +280,11 @@ int check_moe(const void* hidden, int64_t T, int64_t H, int64_t k, const dflash_
 std::atomic<int> g_measure{DFLASH_STAGE_NONE};
 
 bool measuring() { return g_measure.load(std::memory_order_acquire) != DFLASH_STAGE_NONE; }
+// Whether this call launches the kernel(s) of `stage` (GATE_UP, DOWN, or EXPERTS: the fused
+// verify launch); measurement of EXPERTS launches every expert GEMM kernel of the call.
 bool stage_on(int stage) {
   const int m = g_measure.load(std::memory_order_acquire);
-  return m == DFLASH_STAGE_NONE || m == stage;
+  return m == DFLASH_STAGE_NONE || m == stage || m == DFLASH_STAGE_EXPERTS;
 }
 
 // One W4 GEMM over the work table: the LDS-tiled kernel for long prefill, else
@@ -309,6 +336,21 @@ bool verify_fits(const MoeShapes& S, bool route, dflash::VerifyParams* gu, dflas
          verify_layout(kModeDown, T, I, H, E, k, sh, 0, dn);
 }
 
+// Fused layer launch (gate/up and down in one kernel, w4_layer_kernel): a verify block
+// that routes in the gate/up prologue, one scale dtype for both banks, a grid of whole
+// XCDs.  Fills the LDS layouts of both phases.
+std::atomic<int> g_fused_layer{0};  // dflash_set_fused_layer (process-wide)
+
+bool layer_fits(const MoeShapes& S, const dflash::VerifyParams& vgu, dflash::VerifyParams* lgu,
+                dflash::VerifyParams* ldn) {
+  using namespace dflash;
+  if (!g_fused_layer.load(std::memory_order_acquire)) return false;
+  if (!vgu.route || S.gu_f32 != S.dn_f32) return false;
+  if (cu_count() % kXcds != 0 || xcc_count() != kXcds) return false;
+  return layer_layout(static_cast<int>(S.T), static_cast<int>(S.H), static_cast<int>(S.I), static_cast<int>(S.E),
+                      static_cast<int>(S.k), S.shared ? 1 : 0, lgu, ldn);
+}
+
 // Routing outputs the gate/up launch writes when it routes in its prologue.
 struct RouteOut {
   bool logits_given;  // the caller's logits (valid in measurement mode too)
@@ -320,9 +362,13 @@ struct RouteOut {
   int32_t* offsets;
 };
 
-int run_verify(const MoeShapes& S, dflash::VerifyParams gu, dflash::VerifyParams dn, const RouteOut& ro,
-               const int32_t* inv, const float* wts, void* ws, const MoeLayout& L, const dflash_w4* gate_up,
-               const dflash_w4* down, const dflash_w4* sgu, const dflash_w4* sdn, void* out, hipStream_t stream) {
+// `layer`: the fused launch's two phase layouts (layer_fits), or null.  A call that fits the
+// fused launch runs it, except in measurement of one stage (GATE_UP or DOWN alone) or without
+// the caller's logits in measurement mode, which run the two verify launches instead.
+int run_verify(const MoeShapes& S, dflash::VerifyParams gu, dflash::VerifyParams dn, const dflash::VerifyParams* layer,
+               const RouteOut& ro, const int32_t* inv, const float* wts, void* ws, const MoeLayout& L,
+               const dflash_w4* gate_up, const dflash_w4* down, const dflash_w4* sgu, const dflash_w4* sdn, void* out,
+               hipStream_t stream) {
   using namespace dflash;
   const int T = static_cast<int>(S.T), H = static_cast<int>(S.H), I = static_cast<int>(S.I);
   W4StreamParams p{};
@@ -368,14 +414,17 @@ int run_verify(const MoeShapes& S, dflash::VerifyParams gu, dflash::VerifyParams
     gu.slot_w_out = at<float>(ws, L.route.slot_w);
     gu.tok_out = at<int32_t>(ws, L.route.tok);
   }
-  // the routing gate/up launch also plans the down launch's prologue (same workspace, next launch)
+  const int stage = g_measure.load(std::memory_order_acquire);
+  const bool fused = layer && gu.route && (stage == DFLASH_STAGE_NONE || stage == DFLASH_STAGE_EXPERTS);
+  // the routing gate/up launch also plans the down launch's prologue (same workspace, next
+  // launch); a layer that fits the fused launch writes no plan, in measurement mode neither
   const int grid = cu_count();
-  if (gu.route && grid <= kDownPlanMaxGrid) {
+  if (gu.route && !layer && grid <= kDownPlanMaxGrid) {
     gu.down_plan = at<int4>(ws, L.down_plan);
     gu.down_grid = grid;
     gu.down_strips = H / 32;
   }
-  if (stage_on(DFLASH_STAGE_GATE_UP)) launch_w4_verify(kModeGateUp, S.gu_f32, grid, gu, stream);
+  if (!fused && stage_on(DFLASH_STAGE_GATE_UP)) launch_w4_verify(kModeGateUp, S.gu_f32, grid, gu, stream);
   if (int r = launch_status("gate_up")) return r;
 
   // down: N = H rows over K = I, routing-weight epilogue into y, then the combine
@@ -402,8 +451,40 @@ int run_verify(const MoeShapes& S, dflash::VerifyParams gu, dflash::VerifyParams
   // a plan exists only when this call's gate/up launch wrote one (measurement mode timing the
   // down launch alone keeps the work table's pass count)
   dn.down_plan = gu.down_plan && stage_on(DFLASH_STAGE_GATE_UP) ? gu.down_plan : nullptr;
-  if (stage_on(DFLASH_STAGE_DOWN)) launch_w4_verify(kModeDown, S.dn_f32, grid, dn, stream);
-  if (int r = launch_status("down")) return r;
+  if (fused) {
+    // both phases in one launch: the layer layouts, this call's parameters and routing outputs
+    VerifyParams lgu = layer[0], ldn = layer[1];
+    const int route_mode = lgu.route;
+    lgu.g = gu.g;
+    lgu.E = gu.E;
+    lgu.logits = gu.logits;
+    lgu.ids = gu.ids;
+    lgu.wts = gu.wts;
+    lgu.perm = gu.perm;
+    lgu.inv = gu.inv;
+    lgu.offsets = gu.offsets;
+    lgu.meta_out = gu.meta_out;
+    lgu.pass_table_out = gu.pass_table_out;
+    lgu.slot_w_out = gu.slot_w_out;
+    lgu.tok_out = gu.tok_out;
+    lgu.route = route_mode;
+    ldn.g = dn.g;
+    ldn.E = dn.E;
+    for (VerifyParams* v : {&lgu, &ldn}) {
+      v->down_plan = nullptr;
+      v->ready = at<int32_t>(ws, L.ready);
+      v->done = at<int32_t>(ws, L.done);
+      v->ready_stride = L.ready_stride;
+      v->chunks = grid / kXcds;
+      v->err = at<int32_t>(ws, L.err);
+      v->ready_target = I / 16;  // gate/up units (16-column pairs) per pass
+    }
+    launch_w4_layer(S.gu_f32, grid, lgu, ldn, stream);
+    if (int r = launch_status("layer")) return r;
+  } else {
+    if (stage_on(DFLASH_STAGE_DOWN)) launch_w4_verify(kModeDown, S.dn_f32, grid, dn, stream);
+    if (int r = launch_status("down")) return r;
+  }
 
   if (measuring()) return DFLASH_OK;
   // the verify down launch leaves y unweighted: the combine applies the routing weights
@@ -788,7 +869,8 @@ int dflash_moe_experts_w4a16(const void* hidden, int64_t tokens, int64_t hidden_
     if (!measuring()) dflash::launch_table_prep(t, st);
     if (int r = launch_status("table_prep")) return r;
     if (verify)
-      return run_verify(S, vgu, vdn, RouteOut{}, inv_perm, topk_weights, workspace, L, gate_up, down, shared_gate_up,
+      return run_verify(S, vgu, vdn, nullptr, RouteOut{}, inv_perm, topk_weights, workspace, L, gate_up, down,
+                        shared_gate_up,
                         shared_down, out, st);
     return run_experts(S, inv_perm, workspace, L, gate_up, down, shared_gate_up, shared_down, out, st);
   } catch (...) {
@@ -834,6 +916,8 @@ static int moe_w4a16_body(const void* hidden, int64_t tokens, int64_t hidden_siz
     dflash::VerifyParams vgu{}, vdn{};
     const bool verify = tokens > 0 && verify_fits(S, small, &vgu, &vdn);
     if (int r = check_tiled_moe(S, verify)) return r;
+    dflash::VerifyParams layer[2];
+    const bool fused = verify && layer_fits(S, vgu, &layer[0], &layer[1]);
     float* logits = router_logits ? const_cast<float*>(router_logits)
                                   : (logits_out ? logits_out : at<float>(workspace, L.logits));
     dflash::FrontParams f{};
@@ -854,6 +938,10 @@ static int moe_w4a16_body(const void* hidden, int64_t tokens, int64_t hidden_siz
       f.zero = at<uint32_t>(workspace, L.route.counts);
       f.zero_words = dflash::route_zero_words(T, E);
       f.n_zero = static_cast<int>(std::min<int64_t>(256, (f.zero_words + 2047) / 2048));
+    } else if (fused) {  // the fused launch's counters and error word start at zero
+      f.zero = at<uint32_t>(workspace, L.ready);
+      f.zero_words = static_cast<int64_t>(L.ready_words);
+      f.n_zero = 1;
     }
     if (!measuring()) dflash::launch_front(f, st);
     if (int r = launch_status("front")) return r;
@@ -865,7 +953,7 @@ static int moe_w4a16_body(const void* hidden, int64_t tokens, int64_t hidden_siz
     }
     if (tokens == 0) return DFLASH_OK;
     if (verify)
-      return run_verify(S, vgu, vdn,
+      return run_verify(S, vgu, vdn, fused ? layer : nullptr,
                         RouteOut{router_logits != nullptr, logits, topk_ids, topk_weights, perm, inv_perm, expert_offsets},
                         inv_perm, topk_weights, workspace, L, gate_up, down, shared_gate_up, shared_down, out, st);
     return run_experts(S, inv_perm, workspace, L, gate_up, down, shared_gate_up, shared_down, out, st);
@@ -896,8 +984,32 @@ int dflash_moe_w4a16_noalloc(const void* hidden, int64_t tokens, int64_t hidden_
                         perm, inv_perm, expert_offsets, nullptr, 0, true, stream);
 }
 
+int64_t dflash_moe_fused_status_offset(int64_t tokens, int64_t hidden_size, int64_t inter_size, int64_t experts,
+                                       int64_t top_k, int64_t group_size, int has_shared) {
+  try {
+    if (tokens <= 0 || check_route_args(tokens, experts, top_k) != DFLASH_OK) return -1;
+    if (hidden_size <= 0 || hidden_size % 512 || inter_size <= 0 || inter_size % 512) return -1;
+    const MoeShapes S{tokens, hidden_size, inter_size, experts, top_k, group_size, group_size, has_shared != 0,
+                      false, false, true, false};
+    const bool small = dflash::route_small_fits(static_cast<int>(tokens), static_cast<int>(experts),
+                                                static_cast<int>(top_k));
+    dflash::VerifyParams vgu{}, vdn{}, layer[2];
+    if (!verify_fits(S, small, &vgu, &vdn) || !layer_fits(S, vgu, &layer[0], &layer[1])) return -1;
+    return static_cast<int64_t>(moe_layout(S.T, S.H, S.I, S.E, S.k, S.shared).err);
+  } catch (...) {
+    return -1;
+  }
+}
+
+int dflash_set_fused_layer(int enable) {
+  if (enable != 0 && enable != 1) return fail(DFLASH_ERR_INVALID_ARGUMENT, "enable must be 0 or 1");
+  g_fused_layer.store(enable, std::memory_order_release);
+  return DFLASH_OK;
+}
+
 int dflash_set_measure_stage(int stage) {
-  if (stage != DFLASH_STAGE_NONE && stage != DFLASH_STAGE_GATE_UP && stage != DFLASH_STAGE_DOWN)
+  if (stage != DFLASH_STAGE_NONE && stage != DFLASH_STAGE_GATE_UP && stage != DFLASH_STAGE_DOWN &&
+      stage != DFLASH_STAGE_EXPERTS)
     return fail(DFLASH_ERR_INVALID_ARGUMENT, "unknown stage");
   g_measure.store(stage, std::memory_order_release);
   return DFLASH_OK;

@@ -193,11 +193,30 @@ struct VerifyParams {
   // launch (null: neither).  down_grid / down_strips: the down launch's grid and strips.
   int4* down_plan;
   int down_grid, down_strips;
+  // fused layer launch (w4_layer_kernel): pass P belongs to part x = P % 8 (part-local index
+  // j = P / 8), which the workgroups running on XCD x take, `chunks` contiguous unit ranges
+  // per phase, claimed from the part's queues.  Per part a block of ready_stride words:
+  // per-pass counts of finished gate/up units [j] (a down range waits for ready_target), then
+  // the gate/up and the down queue (its last two words).  done counts the workgroups past
+  // their last wait; the last one returns every word to zero (zero on entry, left zero).
+  // err[0] gets bit 0 when a workgroup reads an XCD id above 7, bit 1 when a wait gave up.
+  int fused;
+  int32_t* ready;
+  int32_t* done;
+  int32_t* err;
+  int ready_stride, ready_target, chunks;
 };
 // LDS bytes and layout of one verify launch; false when it does not fit (the
 // caller keeps the separate routing / streaming kernels then).
 bool verify_layout(int mode, int T, int K, int N, int E, int k, int has_shared, int route, VerifyParams* vp);
 void launch_w4_verify(int mode, bool fp32_scales, int grid, const VerifyParams& vp, hipStream_t stream);
+// Gate/up (routing in its prologue) and down in one launch: LDS layouts of both phases
+// (pass descriptors and slot tokens shared, the rest reused); false when they do not fit
+// or the block cannot route in the prologue.  For devices of 8 XCDs; the grid is the CU
+// count, chunks = grid / 8.
+constexpr int kXcds = 8;
+bool layer_layout(int T, int H, int I, int E, int k, int has_shared, VerifyParams* gu, VerifyParams* dn);
+void launch_w4_layer(bool fp32_scales, int grid, const VerifyParams& gu, const VerifyParams& dn, hipStream_t stream);
 // LDS-tiled kernel for long prefill (w4_tile.hip): 96-row passes, column tiles of 512
 // (p.strips = I / 256 for gate_up, H / 512 for down), K % 512 == 0; its gate_up writes one
 // -136*sum(h) per 128 columns and its down reads them that way; its down writes weighted

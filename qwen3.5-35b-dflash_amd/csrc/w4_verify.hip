@@ -58,11 +58,68 @@ constexpr int kVLds = 158 * 1024;  // one persistent workgroup per CU
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
-__device__ __forceinline__ void dma16(buf_rsrc r, void* dst, uint32_t voff, uint32_t soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)dst, 16, static_cast<int>(voff), static_cast<int>(soff), 0, 0);
+// Cache policy of a vector memory load: sc1 (device scope) makes it skip the CU's L1, so it
+// reads this XCD's L2, where other CUs of the XCD left their stores.  (sc0 alone, workgroup
+// scope, may still hit in L1.)
+constexpr int kCacheSc1 = 16;
+
+__device__ __forceinline__ void dma16(buf_rsrc r, void* dst, uint32_t voff, uint32_t soff, int cpol = 0) {
+  if (cpol == kCacheSc1)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)dst, 16, static_cast<int>(voff), static_cast<int>(soff), 0,
+                                             kCacheSc1);
+  else
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)dst, 16, static_cast<int>(voff), static_cast<int>(soff), 0, 0);
 }
-__device__ __forceinline__ void dma4(buf_rsrc r, void* dst, uint32_t voff, uint32_t soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)dst, 4, static_cast<int>(voff), static_cast<int>(soff), 0, 0);
+__device__ __forceinline__ void dma4(buf_rsrc r, void* dst, uint32_t voff, uint32_t soff, int cpol = 0) {
+  if (cpol == kCacheSc1)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)dst, 4, static_cast<int>(voff), static_cast<int>(soff), 0,
+                                             kCacheSc1);
+  else
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)dst, 4, static_cast<int>(voff), static_cast<int>(soff), 0, 0);
+}
+
+// XCD id of the executing workgroup (hardware register).
+__device__ __forceinline__ unsigned xcc_id() {
+  unsigned v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return v & 0xFu;
+}
+
+
+// Polls a workgroup may spend waiting over its whole down range (~0.1-0.4 s).
+constexpr int kSpinBudget = 200000;
+
+// Count word of part-local pass j of part x, and the part's gate/up (phase 0) and down
+// (phase 1) queues, its last two words: each part's words fill cache lines of their own.
+__device__ __forceinline__ int32_t* ready_word(const VerifyParams& vp, int part, int j) {
+  return vp.ready + part * vp.ready_stride + j;
+}
+__device__ __forceinline__ int32_t* queue_word(const VerifyParams& vp, int part, int phase) {
+  return vp.ready + part * vp.ready_stride + vp.ready_stride - 2 + phase;
+}
+
+// The unit range of a verify_gemm call: part `part` of `parts` (pass P is part P % parts's
+// local pass P / parts), its range `rank` of `ranks` contiguous ones.
+struct Split {
+  int part, parts, rank, ranks;
+};
+
+// Bounded wait (one thread) until each of the n count words of consecutive part-local passes
+// reads `target` finished gate/up units (device-scope atomics and loads: the load skips L1,
+// and the count is exact once it reads the target).  Every poll spends one of the workgroup's
+// budget (returned: what is left); once it is spent the wait sets err bit 1 and returns at
+// once, now and at every later call (the launch then ends with wrong down rows, never hangs).
+__device__ __noinline__ int wait_ready(int32_t* words, int n, int target, int32_t* err, int budget) {
+  for (int j = 0; j < n; ++j) {
+    while (__hip_atomic_load(words + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+      if (--budget < 0) {
+        __hip_atomic_fetch_or(err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return budget;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  return budget;
 }
 
 // Opaque to the optimiser: the value must exist in registers at this point.
@@ -575,9 +632,11 @@ __device__ __forceinline__ int verify_passes(const VerifyParams& vp, char* lds) 
   return ld_const(vp.g.meta, 1);
 }
 
-// The streaming GEMM of one verify launch over `total_passes` passes.
+// The streaming GEMM of one verify launch over `total_passes` passes: the units of range
+// sp.rank of part sp.part (linear mode: every workgroup's strided share).
 template <int kMode, int kNKB, typename ScaleT>
-__device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, const int total_passes) {
+__device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, const int total_passes,
+                                            const Split sp) {
   const W4StreamParams& p = vp.g;
   constexpr int kK = kNKB * 128;
   constexpr int kRS = kK * 2 + 16;                  // LDS row stride (bytes) of an activation row
@@ -597,7 +656,13 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
   f32x4* lds_part = reinterpret_cast<f32x4*>(lds + vp.lds_part);  // [wave][2][64]
 
   const int strips = p.strips;
-  const int64_t total_units = static_cast<int64_t>(total_passes) * strips;
+  // fused layer launch: part x's passes (global index P = x + 8 j) and a claimed range of
+  // them; else one part, one range per workgroup.  Below, a pass index is part-local (j)
+  // unless named global.
+  const int parts = sp.parts, part = sp.part, rank = sp.rank, ranks = sp.ranks;
+  const int local_passes = total_passes > part ? (total_passes - part + parts - 1) / parts : 0;
+  auto gpass = [&](int j) { return part + parts * j; };
+  const int64_t total_units = static_cast<int64_t>(local_passes) * strips;
   // linear mode: workgroup b runs units b, b + G, b + 2G, ... (G = grid), so at any moment the
   // workgroups stream one contiguous window of the weights (contiguous ranges per workgroup
   // leave ~2048 streams a fixed stride apart, which streamed up to 10% slower); its virtual
@@ -609,8 +674,8 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
     ub = b * q + min(b, r);
     ue = ub + q + (b < r ? 1 : 0);
   } else {
-    ub = static_cast<int>(total_units * blockIdx.x / gridDim.x);
-    ue = static_cast<int>(total_units * (blockIdx.x + 1) / gridDim.x);
+    ub = static_cast<int>(total_units * rank / ranks);
+    ue = static_cast<int>(total_units * (rank + 1) / ranks);
   }
   // the unit that virtual unit v of this workgroup's range stands for
   auto unit_of = [&](int v) {
@@ -638,19 +703,26 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
     plan_d0 = ld_const_int4(vp.down_plan, b3 + 1);
     plan_d1 = ld_const_int4(vp.down_plan, b3 + 2);
   }
+  auto lds_desc = [&](int i) -> int4 {
+    const int4 v = lds_pdesc[i];
+    return make_int4(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
+                     __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w));
+  };
+  // descriptor of global pass P before the chunk is staged: a fused launch holds every pass
+  // in LDS since its routing prologue (the work table in memory is another XCD's to write)
   auto early_desc = [&](int P) -> int4 {
+    if (vp.fused) return lds_desc(P);
     return P == plan_p ? plan_d0 : P == plan_p + 1 ? plan_d1 : ld_const_int4(p.pass_table, P);
   };
   // pass descriptors: all of them after in-kernel routing, else the chunk's (staged below)
   int pd_base = 0;
-  auto pass_desc = [&](int P) -> int4 {
-    if (kMode == kModeLinear) return make_int4(0, 0, p.M, P * 16);
-    const int4 v = lds_pdesc[P - pd_base];
-    return make_int4(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
-                     __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w));
+  auto pass_desc = [&](int j) -> int4 {
+    if (kMode == kModeLinear) return make_int4(0, 0, p.M, j * 16);
+    return lds_desc(vp.fused ? gpass(j) : j - pd_base);
   };
 
   const bool chunked = kMode == kModeDown || (kMode == kModeGateUp && vp.gather);
+  int spin_budget = kSpinBudget;  // fused down: polls left to this workgroup's waits (thread 0)
   const int chunk_passes = chunked ? vp.chunk_passes : max(P_last - P_first + 1, 1);
   for (int Pc = P_first; Pc <= P_last; Pc += chunk_passes) {
     const int Pc_end = min(P_last + 1, Pc + chunk_passes);
@@ -711,7 +783,7 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
         // before the staging barrier the descriptor comes from the work table (s_load),
         // except after in-kernel routing, whose table is only in LDS
         const int4 d = staged || (kMode == kModeGateUp && vp.route) || kMode == kModeLinear
-                           ? pass_desc(P) : early_desc(P);
+                           ? pass_desc(P) : early_desc(gpass(P));
         const bool shared = kMode != kModeLinear && d.x < 0;
         const int64_t e = kMode == kModeLinear ? 0 : d.x;
         const uint8_t* wbase = shared ? p.w_shared : p.w + e * p.w_stride;
@@ -791,30 +863,40 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
         // loads so the prologue's weight loads are not waited for ahead of them
         pd_base = Pc;
         const int npass = Pc_end - Pc;
-        const buf_rsrc tr = make_rsrc(p.pass_table, static_cast<uint32_t>(total_passes) * 16);
-        if (wave == 0)
-          dma16(tr, lds_pdesc, static_cast<uint32_t>(min(Pc + lane, total_passes - 1) * 16), 0);
+        if (!vp.fused) {
+          const buf_rsrc tr = make_rsrc(p.pass_table, static_cast<uint32_t>(total_passes) * 16);
+          if (wave == 0)
+            dma16(tr, lds_pdesc, static_cast<uint32_t>(min(Pc + lane, total_passes - 1) * 16), 0);
+        } else {
+          // fused launch: the chunk's h rows are written by this XCD's workgroups during this
+          // launch; wait until every gate/up unit of each of its passes has been counted
+          if (tid == 0)
+            spin_budget = wait_ready(ready_word(vp, part, Pc), Pc_end - Pc, vp.ready_target, vp.err, spin_budget);
+          __syncthreads();
+        }
+        // a fused launch reads h through the XCD's L2 (its writers are other CUs of this XCD)
+        const int cpol = vp.fused ? kCacheSc1 : 0;
         const int hrows = p.T * p.top_k + (p.has_shared ? p.T : 0);
         const buf_rsrc hr = make_rsrc(p.act, static_cast<uint32_t>(hrows) * kK * 2);
         constexpr int kBlk = kK / 512;
         for (int i = wave; i < npass * 16 * kBlk; i += kVWaves) {
           const int rr = i / kBlk, bl = i - rr * kBlk;
-          const int4 d = early_desc(Pc + rr / 16);
+          const int4 d = early_desc(gpass(Pc + rr / 16));
           const int base = d.x < 0 ? p.T * p.top_k : d.y;
           const int row = base + min(d.w + (rr & 15), d.z - 1);
           dma16(hr, lds_a + rr * kRS + bl * 1024, static_cast<uint32_t>(lane * 16),
-                static_cast<uint32_t>((row * kK + bl * 512) * 2));
+                static_cast<uint32_t>((row * kK + bl * 512) * 2), cpol);
         }
         constexpr int kPartRow = kNKB * 8;  // partials per h row
         const buf_rsrc pr = make_rsrc(p.act_neg, static_cast<uint32_t>(hrows) * kPartRow * 4);
         for (int i = wave; i < npass * 2 * kNKB; i += kVWaves) {  // 64 partials per load, 2 kNKB per pass
           const int pass = i / (2 * kNKB), j = i - pass * 2 * kNKB;
-          const int4 d = early_desc(Pc + pass);
+          const int4 d = early_desc(gpass(Pc + pass));
           const int base = d.x < 0 ? p.T * p.top_k : d.y;
           const int f = 64 * j + lane, rr = f / kPartRow;
           const int row = base + min(d.w + rr, d.z - 1);
           dma4(pr, lds_hpart + pass * 16 * kPartRow + 64 * j,
-               static_cast<uint32_t>((row * kPartRow + f % kPartRow) * 4), 0);
+               static_cast<uint32_t>((row * kPartRow + f % kPartRow) * 4), 0, cpol);
         }
       }
       wait_vmem();
@@ -934,7 +1016,93 @@ template <int kMode, int kNKB, typename ScaleT>
 __global__ __launch_bounds__(512) void w4_verify_kernel(VerifyParams vp) {
   __shared__ __attribute__((aligned(16))) char lds[kVLds];
   const int total_passes = verify_passes<kMode, kNKB>(vp, lds);
-  verify_gemm<kMode, kNKB, ScaleT>(vp, lds, total_passes);
+  verify_gemm<kMode, kNKB, ScaleT>(vp, lds, total_passes,
+                                   Split{0, 1, static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x)});
+}
+
+// After gate/up range `rank` of part `part` (the split verify_gemm made): every store of the
+// workgroup has reached the XCD's L2 (stores are acknowledged there; L1 writes through), then
+// each pass the range touched gets the number of its units the range finished added to its
+// count, which the down ranges of the part poll.  The workgroup's LDS is free afterwards.
+__device__ __forceinline__ void publish_ready(const VerifyParams& vp, int total_passes, int part, int rank,
+                                              int ranks) {
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's h and partial stores are acknowledged by L2
+  __syncthreads();
+  const int strips = vp.g.strips;
+  const int local_passes = total_passes > part ? (total_passes - part + kXcds - 1) / kXcds : 0;
+  const int64_t total_units = static_cast<int64_t>(local_passes) * strips;
+  const int ub = static_cast<int>(total_units * rank / ranks), ue = static_cast<int>(total_units * (rank + 1) / ranks);
+  if (ue > ub) {
+    for (int j = ub / strips + static_cast<int>(threadIdx.x); j <= (ue - 1) / strips; j += kVThreads) {
+      const int n = min(ue, (j + 1) * strips) - max(ub, j * strips);
+      __hip_atomic_fetch_add(ready_word(vp, part, j), n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __syncthreads();
+}
+
+// After the workgroup's last claim came back empty (every wait of it has ended): the last
+// workgroup of the grid to get here knows every range of every part finished, and returns
+// all counts, queues and the done count to zero for the next launch on this workspace.
+__device__ __forceinline__ void reset_ready(const VerifyParams& vp, int* lds_flag) {
+  if (threadIdx.x == 0)
+    *lds_flag = __hip_atomic_fetch_add(vp.done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                static_cast<int>(gridDim.x) - 1;
+  __syncthreads();
+  if (*lds_flag) {
+    for (int i = static_cast<int>(threadIdx.x); i < kXcds * vp.ready_stride; i += kVThreads)
+      __hip_atomic_store(vp.ready + i, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) __hip_atomic_store(vp.done, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// The routed-MoE layer's expert FFN in one launch: routing prologue, gate/up, then down.  Pass
+// P belongs to part P % 8 in both phases, and only workgroups running on XCD P % 8 (read from
+// the hardware, whatever the dispatch order) take ranges of it, so a down range waits only on
+// gate/up work of its own XCD: counts and h rows meet in that XCD's L2, and nothing crosses
+// XCDs inside the launch.  The combine that sums each token's slots over all XCDs stays a
+// launch of its own.  Ranges are claimed from the part's queues (gate/up first, then down,
+// the next claim in flight during a range), so a part's gate/up ranges all go to workgroups
+// that finish them before any down range of theirs: every wait ends once each XCD runs a
+// workgroup, whatever the residency, and a wait that does not end gives up after its budget.
+template <int kNKBg, int kNKBd, typename ScaleT>
+__global__ __launch_bounds__(512) void w4_layer_kernel(VerifyParams gu, VerifyParams dn) {
+  __shared__ __attribute__((aligned(16))) char lds[kVLds];
+  __shared__ int bcast;
+  const int tid = threadIdx.x;
+  const int part = static_cast<int>(xcc_id());
+  if (part >= kXcds) {  // not an 8-XCD device: take no range (the waits of the others give up)
+    if (tid == 0) __hip_atomic_fetch_or(gu.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    reset_ready(gu, &bcast);
+    return;
+  }
+  // thread 0 claims; the value reaches the workgroup through LDS
+  auto claim = [&](int phase) {
+    return __hip_atomic_fetch_add(queue_word(gu, part, phase), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  auto share = [&](int v) {
+    if (tid == 0) bcast = v;
+    __syncthreads();
+    const int c = bcast;
+    __syncthreads();
+    return c;
+  };
+  int next_gu = 0, next_dn = 0;
+  if (tid == 0) {  // both first claims travel during the routing prologue
+    next_gu = claim(0);
+    next_dn = claim(1);
+  }
+  const int total_passes = verify_passes<kModeGateUp, kNKBg>(gu, lds);
+  for (int c = share(next_gu); c < gu.chunks; c = share(next_gu)) {
+    if (tid == 0) next_gu = claim(0);
+    verify_gemm<kModeGateUp, kNKBg, ScaleT>(gu, lds, total_passes, Split{part, kXcds, c, gu.chunks});
+    publish_ready(gu, total_passes, part, c, gu.chunks);
+  }
+  for (int c = share(next_dn); c < dn.chunks; c = share(next_dn)) {
+    if (tid == 0) next_dn = claim(1);
+    verify_gemm<kModeDown, kNKBd, ScaleT>(dn, lds, total_passes, Split{part, kXcds, c, dn.chunks});
+  }
+  reset_ready(gu, &bcast);
 }
 
 // ---------------------------------------------------------------------------
@@ -1058,6 +1226,88 @@ void launch_w4_verify(int mode, bool fp32_scales, int grid, const VerifyParams& 
   }
 #undef DFLASH_VERIFY_K
 #undef DFLASH_VERIFY
+}
+
+bool layer_layout(int T, int H, int I, int E, int k, int has_shared, VerifyParams* gu, VerifyParams* dn) {
+  // instantiated shapes: gate/up over H in {512, 1024, 2048}, down over I in {512, 1024}
+  if ((H != 512 && H != 1024 && H != 2048) || (I != 512 && I != 1024)) return false;
+  if (T <= 0 || T > 32 || k <= 0 || H % kVStrip) return false;
+  auto al = [](int v) { return (v + 15) & ~15; };
+  const int part = kVWaves * 2 * 64 * 16;
+  int off = 0;
+  auto take = [&](int bytes) {
+    const int o = off;
+    off += al(bytes);
+    return o;
+  };
+  // shared by both phases: every pass descriptor and the token of every slot row (routing)
+  const int tpasses = (T + 15) / 16;
+  const int pd_cap = std::min(E, T * k) * tpasses + (has_shared ? tpasses : 0);
+  const int pdesc = take(pd_cap * 16), tok = take(T * k * 4);
+  const int u0 = off;
+  // gate/up phase: all T x rows, their -136*sum terms, the routing scratch / split partials
+  *gu = VerifyParams{};
+  const int rs_g = 2 * H + 16, nkb_g = H / 128;
+  gu->a_rows = T;
+  gu->pd_cap = pd_cap;
+  gu->lds_pdesc = pdesc;
+  gu->lds_tok = tok;
+  gu->lds_a = take(T * rs_g);
+  gu->lds_neg = take(((T * nkb_g + 63) & ~63) * 4);
+  const int tpad = (T + 3) & ~3;
+  const int row_scratch = (256 + 512 + 512 + 12) * 4 + E * tpad;
+  const int scratch = al(((E + 3) & ~3) * 4) + al(((T * k + 3) & ~3) * 4) + 96 + E * tpad;
+  if (E <= 256 && k <= 16 && T * k <= 512) {
+    gu->route = 2;
+    gu->lds_part = gu->lds_scratch = take(std::max(part, row_scratch));
+  } else if (E <= 2 * kVThreads) {
+    gu->route = 1;
+    gu->lds_part = gu->lds_scratch = take(std::max(part, al(scratch)));
+  } else {
+    return false;
+  }
+  gu->lds_bytes = off;
+  if (off > kVLds) return false;
+  // down phase over the same bytes after the descriptors: chunks of h rows and their partials
+  off = u0;
+  *dn = VerifyParams{};
+  const int rs_d = 2 * I + 16, nkb_d = I / 128;
+  dn->lds_part = dn->lds_scratch = take(part);
+  const int per_pass = 16 * rs_d + al(16 * nkb_d * 4) + al(16 * nkb_d * 8 * 4);
+  const int cp = std::min(8, (kVLds - off) / per_pass);
+  if (cp < 1) return false;
+  dn->chunk_passes = cp;
+  dn->pd_cap = pd_cap;
+  dn->a_rows = cp * 16;
+  dn->lds_pdesc = pdesc;
+  dn->lds_tok = tok;
+  dn->lds_a = take(cp * 16 * rs_d);
+  dn->lds_neg = take(cp * 16 * nkb_d * 4);
+  dn->lds_wgt = take(cp * 16 * nkb_d * 8 * 4);
+  dn->lds_bytes = off;
+  gu->fused = dn->fused = 1;
+  return off <= kVLds;
+}
+
+void launch_w4_layer(bool fp32_scales, int grid, const VerifyParams& gu, const VerifyParams& dn, hipStream_t stream) {
+  const dim3 g(static_cast<unsigned>(grid)), blk(kVThreads);
+#define DFLASH_LAYER(NG, ND)                                                                             \
+  do {                                                                                                   \
+    if (fp32_scales) hipLaunchKernelGGL((w4_layer_kernel<NG, ND, float>), g, blk, 0, stream, gu, dn);   \
+    else hipLaunchKernelGGL((w4_layer_kernel<NG, ND, uint16_t>), g, blk, 0, stream, gu, dn);            \
+  } while (0)
+#define DFLASH_LAYER_D(NG)                            \
+  do {                                                \
+    if (dn.g.K == 512) DFLASH_LAYER(NG, 4);           \
+    else DFLASH_LAYER(NG, 8);                         \
+  } while (0)
+  switch (gu.g.K) {
+    case 512: DFLASH_LAYER_D(4); break;
+    case 1024: DFLASH_LAYER_D(8); break;
+    default: DFLASH_LAYER_D(16); break;
+  }
+#undef DFLASH_LAYER_D
+#undef DFLASH_LAYER
 }
 
 }  // namespace dflash

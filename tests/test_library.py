@@ -212,6 +212,13 @@ def test_measure_stage_validation(pkg):
     assert lib.dflash_set_measure_stage(0) == 0
 
 
+def test_fused_layer_switch_validation(pkg):
+    lib = pkg._lib.load()
+    assert lib.dflash_set_fused_layer(2) == 1
+    assert "enable" in lib.dflash_last_error().decode()
+    assert lib.dflash_set_fused_layer(0) == 0
+
+
 def test_moe_experts_refuses_malformed_routing(pkg):
     """A caller-given routing is checked for dtype, shape, device and contiguity before its
     pointers reach the kernels (they index the work table and the weights with it)."""
