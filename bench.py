@@ -67,9 +67,7 @@ def log(msg: str) -> None:
 
 def device_bank(pkg, gen, shape, device):
     """Random packed int4 bank generated on the device (uniform bytes = two uniform int4)."""
-    packed = torch.randint(0, 256, (*shape[:-1], shape[-1] // 2), dtype=torch.uint8, device=device, generator=gen)
-    scales = (torch.rand((*shape[:-1], shape[-1] // 128), device=device, generator=gen) * 0.015 + 0.005)
-    return pkg.PackedW4(packed, scales.to(torch.bfloat16).contiguous(), 128)
+    return pkg.synthetic.device_bank(gen, shape, device)
 
 
 def weight_sets(pkg, nsets, device, seed=1234, hidden=2048, inter=512, experts=256, tiled=True):

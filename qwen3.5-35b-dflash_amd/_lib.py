@@ -89,14 +89,19 @@ class DflashError(RuntimeError):
 _LIB = None
 
 
-def load() -> ctypes.CDLL:
-    """Load (once) and type the library; raises if it was not built."""
+def load(path: Path = LIBRARY_PATH) -> ctypes.CDLL:
+    """Load (once) and type the library; raises if it was not built.
+
+    ``path`` selects another build of the same ABI before the first call (the
+    profiling build of ``timeline.py``); once loaded, the library stays.
+    """
     global _LIB
     if _LIB is not None:
+        if path != LIBRARY_PATH and Path(_LIB._name) != path:
+            raise RuntimeError(f"{Path(_LIB._name).name} is already loaded; {path.name} must be loaded first")
         return _LIB
-    path = LIBRARY_PATH
     if not path.is_file():
-        raise RuntimeError(f"libdflash_hip.so not found at {path}; build it with build.py (hipcc, gfx950)")
+        raise RuntimeError(f"{path.name} not found at {path}; build it with build.py (hipcc, gfx950)")
     lib = ctypes.CDLL(str(path))
     for name, (restype, argtypes) in SIGNATURES.items():
         fn = getattr(lib, name)

@@ -3,6 +3,9 @@
 ``python build.py`` from this directory, or ``build()`` from Python.  Each
 translation unit is compiled in parallel with hipcc, then linked into one
 shared library next to this file; the library is replaced atomically.
+``python build.py --timeline`` (``build(timeline=True)``) builds the profiling
+variant ``libdflash_hip_timeline.so`` instead: the same kernels with phase
+timestamps (``-DDFLASH_TIMELINE``), loaded only by ``timeline.py``.
 """
 from __future__ import annotations
 
@@ -15,6 +18,7 @@ from pathlib import Path
 
 PACKAGE_DIR = Path(__file__).resolve().parent
 LIBRARY = PACKAGE_DIR / "libdflash_hip.so"
+TIMELINE_LIBRARY = PACKAGE_DIR / "libdflash_hip_timeline.so"
 SOURCES = ("csrc/api.hip", "csrc/route.hip", "csrc/w4_gemm.hip", "csrc/w4_stream.hip",
            "csrc/w4_tile.hip", "csrc/w4_verify.hip",
            "csrc/repack.hip")
@@ -33,13 +37,15 @@ def _hipcc() -> str:
     return path
 
 
-def build(verbose: bool = False) -> Path:
+def build(verbose: bool = False, timeline: bool = False) -> Path:
     hipcc = _hipcc()
+    target = TIMELINE_LIBRARY if timeline else LIBRARY
+    flags = (*FLAGS, "-DDFLASH_TIMELINE") if timeline else FLAGS
     with tempfile.TemporaryDirectory(prefix="dflash_build_") as tmp:
         objects, procs = [], []
         for src in SOURCES:
             obj = Path(tmp) / (Path(src).stem + ".o")
-            cmd = [hipcc, *FLAGS, "-c", str(PACKAGE_DIR / src), "-o", str(obj)]
+            cmd = [hipcc, *flags, "-c", str(PACKAGE_DIR / src), "-o", str(obj)]
             objects.append(obj)
             procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
         for cmd, proc in procs:
@@ -48,16 +54,16 @@ def build(verbose: bool = False) -> Path:
                 raise RuntimeError(f"hipcc failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
             if verbose and out.strip():
                 print(out)
-        staged = Path(tmp) / LIBRARY.name
+        staged = Path(tmp) / target.name
         link = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(staged)]
         proc = subprocess.run(link, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
         if proc.returncode:
             raise RuntimeError(f"link failed: {' '.join(link)}\n{proc.stdout}")
-        tmp_target = LIBRARY.with_suffix(".so.tmp")
+        tmp_target = target.with_suffix(".so.tmp")
         shutil.copyfile(staged, tmp_target)
-        os.replace(tmp_target, LIBRARY)
-    return LIBRARY
+        os.replace(tmp_target, target)
+    return target
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    print(build(verbose="-v" in sys.argv, timeline="--timeline" in sys.argv))

@@ -1007,6 +1007,15 @@ int dflash_set_fused_layer(int enable) {
   return DFLASH_OK;
 }
 
+#ifdef DFLASH_TIMELINE
+// Profiling build only (timeline.py; not in the product ABI): which 0 = verify launches
+// (2 x 1024 x 16 ticks), 1 = tile launches (2 x 1024 x 8 x 3).
+int dflash_timeline_read(int which, void* host, size_t bytes) {
+  return which == 0 ? dflash::timeline_verify_read(host, bytes) : dflash::timeline_tile_read(host, bytes);
+}
+int dflash_timeline_clear(void) { return dflash::timeline_verify_clear() | dflash::timeline_tile_clear(); }
+#endif
+
 int dflash_set_measure_stage(int stage) {
   if (stage != DFLASH_STAGE_NONE && stage != DFLASH_STAGE_GATE_UP && stage != DFLASH_STAGE_DOWN &&
       stage != DFLASH_STAGE_EXPERTS)

@@ -206,6 +206,13 @@ struct VerifyParams {
   int32_t* err;
   int ready_stride, ready_target, chunks;
 };
+#ifdef DFLASH_TIMELINE
+// Profiling build: phase timestamps of the verify and tile launches (timeline.py).
+int timeline_verify_read(void* host, size_t bytes);
+int timeline_verify_clear();
+int timeline_tile_read(void* host, size_t bytes);
+int timeline_tile_clear();
+#endif
 // LDS bytes and layout of one verify launch; false when it does not fit (the
 // caller keeps the separate routing / streaming kernels then).
 bool verify_layout(int mode, int T, int K, int N, int E, int k, int has_shared, int route, VerifyParams* vp);

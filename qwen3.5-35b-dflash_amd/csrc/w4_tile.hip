@@ -39,6 +39,14 @@ namespace dflash {
 namespace {
 
 constexpr int kTileM = 96;                  // rows per pass (6 subtiles of 16)
+
+// Per-tile times of the profiling build (DFLASH_TIMELINE, loaded only by timeline.py): per
+// launch mode (gate/up, down), workgroup and its first 8 tiles, s_memrealtime ticks (100 MHz)
+// at the tile's start and end and the tile's rows | pass << 16 | (order + 1) << 40.
+#ifdef DFLASH_TIMELINE
+constexpr int kTlWorkgroups = 1024, kTlTiles = 8;
+__device__ unsigned long long g_timeline_tile[2 * kTlWorkgroups * kTlTiles * 3];
+#endif
 constexpr int kMaxSub = kTileM / 16;
 constexpr int kWaves = 8;
 constexpr int kTileN = kWaves * 64;         // output columns per tile
@@ -375,10 +383,29 @@ __global__ __launch_bounds__(512) void w4_tile_kernel(W4StreamParams p) {
   // `total` and the request that returns total - 1 is the launch's last: it resets the
   // queue for the next launch.  Nothing waits on the queue.
   int* queue = const_cast<int*>(p.meta) + (kMode == kModeGateUp ? 2 : 3);
+#ifdef DFLASH_TIMELINE
+  int tl_n = 0;
+#endif
   for (int tile = blockIdx.x; tile < total;) {
     const int i = tile / ntiles;
     const int P = i < sp ? passes - sp + i : i - sp;
+#ifdef DFLASH_TIMELINE
+    unsigned long long* tl = g_timeline_tile +
+        (((kMode == kModeGateUp ? 0 : 1) * kTlWorkgroups + blockIdx.x) * kTlTiles + min(tl_n, kTlTiles - 1)) * 3;
+    if (threadIdx.x == 0 && blockIdx.x < kTlWorkgroups) tl[0] = __builtin_amdgcn_s_memrealtime();
+#endif
     run_tile<kMode, ScaleT>(p, lds, P, tile - i * ntiles);
+#ifdef DFLASH_TIMELINE
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0 && blockIdx.x < kTlWorkgroups) {
+      const int4 d = ld_const_int4(p.pass_table, P);
+      tl[1] = __builtin_amdgcn_s_memrealtime();
+      tl[2] = static_cast<unsigned long long>(min(kTileM, d.z - d.w)) | (static_cast<unsigned long long>(P) << 16) |
+              (static_cast<unsigned long long>(tl_n + 1) << 40);
+    }
+    ++tl_n;
+#endif
     if (threadIdx.x == 0) {
       const int got = __hip_atomic_fetch_add(queue, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (got == total - 1) __hip_atomic_store(queue, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -405,5 +432,17 @@ void launch_w4_tile(int mode, bool fp32_scales, int grid, const W4StreamParams& 
     else hipLaunchKernelGGL((w4_tile_kernel<kModeDown, uint16_t>), g, blk, 0, stream, p);
   }
 }
+
+#ifdef DFLASH_TIMELINE
+int timeline_tile_read(void* host, size_t bytes) {
+  if (bytes != sizeof(g_timeline_tile)) return 1;
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_timeline_tile), bytes) == hipSuccess ? 0 : 1;
+}
+int timeline_tile_clear() {
+  void* ptr = nullptr;
+  if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_timeline_tile)) != hipSuccess) return 1;
+  return hipMemset(ptr, 0, sizeof(g_timeline_tile)) == hipSuccess ? 0 : 1;
+}
+#endif
 
 }  // namespace dflash

@@ -97,6 +97,26 @@ __device__ __forceinline__ unsigned xcc_id() {
 }
 
 
+// Phase timestamps of the profiling build (compiled with DFLASH_TIMELINE, loaded only by
+// timeline.py; the product library has none of it): per separate gate/up (mode 1) or down
+// (mode 2) launch and workgroup, 16 slots of s_memrealtime ticks (100 MHz): 0 start, 1 pass
+// count known (after in-kernel routing), 2 first chunk staged, 3 the XCD id (not a time),
+// 4 + w wave w's k-loop done, 12 the workgroup's partial sums exchanged, 13 end.
+#ifdef DFLASH_TIMELINE
+constexpr int kTlWorkgroups = 1024, kTlSlots = 16;
+__device__ unsigned long long g_timeline_verify[2 * kTlWorkgroups * kTlSlots];
+__device__ __forceinline__ void tl_mark(int mode, int slot, bool lane0_of_every_wave = false) {
+  const bool writer = lane0_of_every_wave ? (threadIdx.x & 63) == 0 : threadIdx.x == 0;
+  if ((mode == kModeGateUp || mode == kModeDown) && writer && blockIdx.x < kTlWorkgroups) {
+    unsigned long long* row = g_timeline_verify + ((mode - 1) * kTlWorkgroups + blockIdx.x) * kTlSlots;
+    row[slot] = __builtin_amdgcn_s_memrealtime();
+    if (slot == 0) row[3] = xcc_id();
+  }
+}
+#else
+__device__ __forceinline__ void tl_mark(int, int, bool = false) {}
+#endif
+
 // Polls a workgroup may spend waiting over its whole down range (~0.1-0.4 s).
 constexpr int kSpinBudget = 200000;
 
@@ -922,6 +942,7 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
         __syncthreads();
       }
       staged = true;
+      if (Pc == P_first && !vp.fused) tl_mark(kMode, 2);
 
       // compute state of the current unit
       int c_ur = -1, P = 0, a_off = 0;
@@ -1003,7 +1024,9 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
         }
       }
     }
+    if (!vp.fused) tl_mark(kMode, 4 + wave, true);
     lds_barrier();  // partial sums of split units are in LDS
+    if (!vp.fused) tl_mark(kMode, 12);
     if (head_unit >= 0) {
       // sum the partials of the waves before this one that share the unit, in wave order
       const int gs = head_unit * kNKB;
@@ -1026,9 +1049,16 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
 template <int kMode, int kNKB, typename ScaleT>
 __global__ __launch_bounds__(512) void w4_verify_kernel(VerifyParams vp) {
   __shared__ __attribute__((aligned(16))) char lds[kVLds];
+  tl_mark(kMode, 0);
   const int total_passes = verify_passes<kMode, kNKB>(vp, lds);
+  tl_mark(kMode, 1);
   verify_gemm<kMode, kNKB, ScaleT>(vp, lds, total_passes,
                                    Split{0, 1, static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x)});
+#ifdef DFLASH_TIMELINE
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  tl_mark(kMode, 13);
+#endif
 }
 
 // After gate/up range `rank` of part `part` (the split verify_gemm made): every store of the
@@ -1320,5 +1350,17 @@ void launch_w4_layer(bool fp32_scales, int grid, const VerifyParams& gu, const V
 #undef DFLASH_LAYER_D
 #undef DFLASH_LAYER
 }
+
+#ifdef DFLASH_TIMELINE
+int timeline_verify_read(void* host, size_t bytes) {
+  if (bytes != sizeof(g_timeline_verify)) return 1;
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_timeline_verify), bytes) == hipSuccess ? 0 : 1;
+}
+int timeline_verify_clear() {
+  void* ptr = nullptr;
+  if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_timeline_verify)) != hipSuccess) return 1;
+  return hipMemset(ptr, 0, sizeof(g_timeline_verify)) == hipSuccess ? 0 : 1;
+}
+#endif
 
 }  // namespace dflash

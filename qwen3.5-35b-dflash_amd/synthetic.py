@@ -27,6 +27,14 @@ def int4_weight(gen: torch.Generator, shape: tuple, group_size: int = 128,
     return PackedW4(packed.to(device), scales.contiguous().to(device), group_size)
 
 
+def device_bank(gen: torch.Generator, shape: tuple, device, group_size: int = 128) -> PackedW4:
+    """Random packed bank generated on the device by ``gen`` (a device generator): uniform bytes
+    (two uniform int4 values each), bf16 scales ``U(0.005, 0.02)``; for benchmark-sized banks."""
+    packed = torch.randint(0, 256, (*shape[:-1], shape[-1] // 2), dtype=torch.uint8, device=device, generator=gen)
+    scales = torch.rand((*shape[:-1], shape[-1] // group_size), device=device, generator=gen) * 0.015 + 0.005
+    return PackedW4(packed, scales.to(torch.bfloat16).contiguous(), group_size)
+
+
 class MoeLayer(NamedTuple):
     hidden: torch.Tensor          # bf16 [T, H]
     router_weight: torch.Tensor   # bf16 [E, H]
