@@ -3,6 +3,9 @@
 // A work tile is one pass (up to 96 rows of one slot: an expert segment or
 // the shared expert) times one column tile of 512 outputs; persistent
 // workgroups (one per CU, 8 waves, 64 columns each) take tiles round robin.
+// The tiles left over after the last full round of the grid run as two
+// half-width pieces each (8 waves, 32 columns each), so that final round
+// spreads over twice as many workgroups.
 // Per 128-column k-block of the reduction:
 //   * every operand reaches LDS by direct-to-LDS buffer loads (no register
 //     staging): the pass's activation rows in MFMA fragment order (1 KB
@@ -42,7 +45,8 @@ constexpr int kTileM = 96;                  // rows per pass (6 subtiles of 16)
 
 // Per-tile times of the profiling build (DFLASH_TIMELINE, loaded only by timeline.py): per
 // launch mode (gate/up, down), workgroup and its first 8 tiles, s_memrealtime ticks (100 MHz)
-// at the tile's start and end and the tile's rows | pass << 16 | (order + 1) << 40.
+// at the tile's start and end and the tile's rows | pass << 16 | (order + 1) << 40 | half << 56
+// (1 for a half-width piece).
 #ifdef DFLASH_TIMELINE
 constexpr int kTlWorkgroups = 1024, kTlTiles = 8;
 __device__ unsigned long long g_timeline_tile[2 * kTlWorkgroups * kTlTiles * 3];
@@ -117,7 +121,8 @@ __device__ __forceinline__ void interleave() {
   }
 }
 
-template <int kMode, typename ScaleT, int NSUB>
+// NF: 16-column weight fragments per wave (4: a 512-column tile; 2: a half-width piece).
+template <int kMode, typename ScaleT, int NSUB, int NF>
 __device__ __forceinline__ void tile_pass(const W4StreamParams& p, const TileLds& lds, const TileCtx& c) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -138,7 +143,7 @@ __device__ __forceinline__ void tile_pass(const W4StreamParams& p, const TileLds
   auto load_w = [&](int kb, auto sw) {
     kb = min(kb, nkb - 1);
 #pragma unroll
-    for (int f = 0; f < 4; ++f) dma16(c.wrs, lds.w[sw] + (wave * 4 + f) * 64, c.woff[f], kb * c.wkb);
+    for (int f = 0; f < NF; ++f) dma16(c.wrs, lds.w[sw] + (wave * 4 + f) * 64, c.woff[f], kb * c.wkb);
     const int g = kb >> gshift;
     // portable: the 4 bytes at the lane's row and group (pair); tiled: the group's 16-column
     // chunk at the lane's even column (a bf16 lane takes its half below)
@@ -146,10 +151,10 @@ __device__ __forceinline__ void tile_pass(const W4StreamParams& p, const TileLds
          p.tiled ? g * 16 * static_cast<int>(sizeof(ScaleT)) : (sizeof(ScaleT) == 4 ? g * 4 : (g & ~1) * 2));
   };
   // this lane's weights and group scales of k-block kb from stage sw
-  auto read_w = [&](uint4 (&wf)[4], float (&sc)[4], int kb, auto sw) {
+  auto read_w = [&](uint4 (&wf)[NF], float (&sc)[NF], int kb, auto sw) {
     const int g = kb >> gshift;
 #pragma unroll
-    for (int f = 0; f < 4; ++f) {
+    for (int f = 0; f < NF; ++f) {
       wf[f] = lds.w[sw][(wave * 4 + f) * 64 + lane];
       const uint32_t bits = lds.s[sw][wave * 64 + f * 16 + lr];
       const bool hi = p.tiled ? (lr & 1) : (g & 1);
@@ -167,33 +172,35 @@ __device__ __forceinline__ void tile_pass(const W4StreamParams& p, const TileLds
   asm volatile("" ::: "memory");
   load_w(1, Idx<1>{});
 
-  f32x4 u[NSUB][4];  // running sums in units of the current k-block's scale
-  float s_prev[4] = {0.f, 0.f, 0.f, 0.f}, s_next[4];
-  uint4 wf[4];       // packed weights of the k-block about to run
-  uint4 bc[4];       // dequantised weights of the k-step about to run
-  uint4 a[NSUB];     // activation fragments of the k-step about to run
+  f32x4 u[NSUB][NF];  // running sums in units of the current k-block's scale
+  float s_prev[NF], s_next[NF];
+  uint4 wf[NF];       // packed weights of the k-block about to run
+  uint4 bc[NF];       // dequantised weights of the k-step about to run
+  uint4 a[NSUB];      // activation fragments of the k-step about to run
+#pragma unroll
+  for (int f = 0; f < NF; ++f) s_prev[f] = 0.f;
 #pragma unroll
   for (int ms = 0; ms < NSUB; ++ms)
 #pragma unroll
-    for (int f = 0; f < 4; ++f) u[ms][f] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int f = 0; f < NF; ++f) u[ms][f] = f32x4{0.f, 0.f, 0.f, 0.f};
   read_w(wf, s_next, 0, Idx<0>{});
 #pragma unroll
-  for (int f = 0; f < 4; ++f) bc[f] = dequant8(wf[f].x);
+  for (int f = 0; f < NF; ++f) bc[f] = dequant8(wf[f].x);
 
   auto step = [&](int kb, auto sa_tag, auto sw_tag) {
     constexpr int sa = decltype(sa_tag)::value, sw = decltype(sw_tag)::value;
     // the activation stage of k-block kb is complete once this wave's loads older than the
-    // last 5 (weights and scales of k-block kb + 1) are
-    dma_barrier<5>();
+    // last NF + 1 (weights and scales of k-block kb + 1) are
+    dma_barrier<NF + 1>();
     load_a(kb + 1, Idx<(sa + 1) % kAStages>{});
     asm volatile("" ::: "memory");
     load_w(kb + 2, Idx<(sw + 2) % kWStages>{});
 #pragma unroll
     for (int ms = 0; ms < NSUB; ++ms) a[ms] = lds.a[sa][ms * 4 * 64 + lane];
     // u <- u * s_prev / s_kb - 136 * sum(a_kb)   (k-block 0: u = -136 * sum)
-    float ratio[4];
+    float ratio[NF];
 #pragma unroll
-    for (int f = 0; f < 4; ++f) {
+    for (int f = 0; f < NF; ++f) {
       ratio[f] = s_prev[f] * __builtin_amdgcn_rcpf(s_next[f]);
       s_prev[f] = s_next[f];
     }
@@ -201,24 +208,24 @@ __device__ __forceinline__ void tile_pass(const W4StreamParams& p, const TileLds
     for (int ms = 0; ms < NSUB; ++ms) {
       const f32x4 start = *reinterpret_cast<const f32x4*>(lds.neg[sa] + ms * 16 + 4 * kq);
 #pragma unroll
-      for (int f = 0; f < 4; ++f) u[ms][f] = u[ms][f] * ratio[f] + start;
+      for (int f = 0; f < NF; ++f) u[ms][f] = u[ms][f] * ratio[f] + start;
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
 #pragma unroll
       for (int ms = 0; ms < NSUB; ++ms) {
 #pragma unroll
-        for (int f = 0; f < 4; ++f) u[ms][f] = mfma16x16x32(a[ms], bc[f], u[ms][f]);
+        for (int f = 0; f < NF; ++f) u[ms][f] = mfma16x16x32(a[ms], bc[f], u[ms][f]);
         if (j < 3) a[ms] = lds.a[sa][(ms * 4 + j + 1) * 64 + lane];
       }
       if (j == 3) read_w(wf, s_next, kb + 1, Idx<(sw + 1) % kWStages>{});
 #pragma unroll
-      for (int f = 0; f < 4; ++f) bc[f] = dequant8(word(wf[f], (j + 1) & 3));
-      // k-step 0 also holds the rescale (16 FMAs per subtile, the first subtile's ahead of all MFMAs),
-      // k-step 3 the next k-block's weight and scale reads
-      if (j == 0) interleave<24, 4 * NSUB, (16 * NSUB + 24) / (4 * NSUB), 2>();
-      else if (j == 3) interleave<0, 4 * NSUB, 3, 2>();
-      else interleave<0, 4 * NSUB, 2, 4>();
+      for (int f = 0; f < NF; ++f) bc[f] = dequant8(word(wf[f], (j + 1) & 3));
+      // k-step 0 also holds the rescale (4 NF FMAs per subtile, the first subtile's ahead of all
+      // MFMAs), k-step 3 the next k-block's weight and scale reads
+      if (j == 0) interleave<6 * NF, NF * NSUB, (4 * NF * NSUB + 6 * NF) / (NF * NSUB), 2>();
+      else if (j == 3) interleave<0, NF * NSUB, 3, 2>();
+      else interleave<0, NF * NSUB, 2, 4>();
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -240,8 +247,10 @@ __device__ __forceinline__ void tile_pass(const W4StreamParams& p, const TileLds
   // epilogue: lane holds rows 16 ms + 4 kq + e of its fragments' column lr
   const int4 d = c.d;
   if (kMode == kModeGateUp) {
-    // h, and -136 * sum(h) per 128 columns: waves 0-3 cover the tile's first 128 columns,
-    // waves 4-7 the second; per-wave row partials meet in LDS (activation stage 0)
+    // h, and -136 * sum(h) per 128 columns: a wave covers 16 H2 columns of the gate and up
+    // halves (H2 = NF / 2), so 8 / H2 consecutive waves cover one 128-column block; per-wave row
+    // partials meet in LDS (activation stage 0)
+    constexpr int H2 = NF / 2, kWavesPerBlock = kWaves / H2;
     float* red = reinterpret_cast<float*>(lds.a[0]);  // [kWaves][kTileM]
     __syncthreads();  // every wave is done reading the activation stages
 #pragma unroll
@@ -254,9 +263,9 @@ __device__ __forceinline__ void tile_pass(const W4StreamParams& p, const TileLds
         const int hrow = c.shared ? p.T * p.top_k + m : d.y + m;
         float part = 0.f;
 #pragma unroll
-        for (int f = 0; f < 2; ++f) {
-          const int col = c.nt * 256 + wave * 32 + f * 16 + lr;
-          const uint16_t hb = f32_to_bf16(silu(u[ms][f][e] * s_prev[f]) * (u[ms][f + 2][e] * s_prev[f + 2]));
+        for (int f = 0; f < H2; ++f) {
+          const int col = c.nt * kWaves * 16 * H2 + wave * 16 * H2 + f * 16 + lr;
+          const uint16_t hb = f32_to_bf16(silu(u[ms][f][e] * s_prev[f]) * (u[ms][f + H2][e] * s_prev[f + H2]));
           if (valid) p.out_bf16[static_cast<int64_t>(hrow) * inter + octet_slot(col)] = hb;
           part += bf16_to_f32(hb);
         }
@@ -265,14 +274,15 @@ __device__ __forceinline__ void tile_pass(const W4StreamParams& p, const TileLds
       }
     }
     __syncthreads();
-    if (tid < 2 * kTileM) {
-      const int half = tid >= kTileM ? 1 : 0, r = tid - half * kTileM;
+    if (tid < H2 * kTileM) {
+      const int half = tid / kTileM, r = tid - half * kTileM;
       if (r < c.rows) {
-        const float* q = red + 4 * half * kTileM + r;
-        const float sum = (q[0] + q[kTileM]) + (q[2 * kTileM] + q[3 * kTileM]);
+        const float* q = red + kWavesPerBlock * half * kTileM + r;
+        float sum = (q[0] + q[kTileM]) + (q[2 * kTileM] + q[3 * kTileM]);
+        if (kWavesPerBlock == 8) sum += (q[4 * kTileM] + q[5 * kTileM]) + (q[6 * kTileM] + q[7 * kTileM]);
         const int m = d.w + r;
         const int hrow = c.shared ? p.T * p.top_k + m : d.y + m;
-        p.out_part[static_cast<int64_t>(hrow) * (inter >> 7) + c.nt * 2 + half] = -kDequantOffset * sum;
+        p.out_part[static_cast<int64_t>(hrow) * (inter >> 7) + c.nt * H2 + half] = -kDequantOffset * sum;
       }
     }
   } else {
@@ -286,17 +296,18 @@ __device__ __forceinline__ void tile_pass(const W4StreamParams& p, const TileLds
         const int yrow = c.shared ? p.T * p.top_k + m : d.y + m;
         const float wgt = c.shared ? p.shared_gate[m] : p.slot_w[d.y + m];
         // weighted, in bf16: halves the y traffic of this launch and the combine's
-        uint16_t* o = reinterpret_cast<uint16_t*>(p.out_f32) + static_cast<int64_t>(yrow) * p.N + c.nt * kTileN +
-                      wave * 64 + lr;
+        uint16_t* o = reinterpret_cast<uint16_t*>(p.out_f32) + static_cast<int64_t>(yrow) * p.N +
+                      c.nt * kWaves * 16 * NF + wave * 16 * NF + lr;
 #pragma unroll
-        for (int f = 0; f < 4; ++f) o[f * 16] = f32_to_bf16(u[ms][f][e] * s_prev[f] * wgt);
+        for (int f = 0; f < NF; ++f) o[f * 16] = f32_to_bf16(u[ms][f][e] * s_prev[f] * wgt);
       }
     }
   }
 }
 
-// One work tile: pass P (up to 96 rows of one slot) times column tile nt.
-template <int kMode, typename ScaleT>
+// One work tile: pass P (up to 96 rows of one slot) times column tile nt of 8 x 16 NF columns
+// (gate/up: 8 x 8 NF of each half).
+template <int kMode, typename ScaleT, int NF>
 __device__ __forceinline__ void run_tile(const W4StreamParams& p, const TileLds& lds, int P, int nt) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -307,10 +318,12 @@ __device__ __forceinline__ void run_tile(const W4StreamParams& p, const TileLds&
   // activation rows: tokens (gate_up) or every routed slot row plus the shared expert's (down)
   const uint32_t act_rows = kMode == kModeGateUp ? p.T : p.T * p.top_k + (p.has_shared ? p.T : 0);
 
-  // weight row of fragment f, column lc (0..15) of this wave
+  // weight row of fragment f, column lc (0..15) of this wave: gate/up fragments f < NF / 2 are
+  // gate rows, the rest the same columns' up rows
+  constexpr int H2 = NF / 2;
   auto wrow = [&](int f, int lc) {
-    return kMode == kModeGateUp ? (f >> 1) * inter + nt * 256 + wave * 32 + (f & 1) * 16 + lc
-                                : nt * kTileN + wave * 64 + f * 16 + lc;
+    return kMode == kModeGateUp ? (f / H2) * inter + nt * kWaves * 16 * H2 + wave * 16 * H2 + (f % H2) * 16 + lc
+                                : nt * kWaves * 16 * NF + wave * 16 * NF + f * 16 + lc;
   };
 
   TileCtx c;
@@ -328,12 +341,14 @@ __device__ __forceinline__ void run_tile(const W4StreamParams& p, const TileLds&
   // a fragment's 16 rows are one tile of the tiled layout (its base is the same in both layouts)
   c.wkb = p.tiled ? 1024u : 64u;
 #pragma unroll
-  for (int f = 0; f < 4; ++f)
+  for (int f = 0; f < NF; ++f)
     c.woff[f] = p.tiled ? static_cast<uint32_t>(wrow(f, 0)) * rb + lane * 16
                         : static_cast<uint32_t>(wrow(f, lr)) * rb + kq * 16;
-  c.soff = p.tiled ? (static_cast<uint32_t>(wrow(lane >> 4, 0)) * static_cast<uint32_t>(ng) +
+  // scale lane: fragment lane / 16 (lanes past the wave's NF fragments repeat its last one)
+  const int sf = min(lane >> 4, NF - 1);
+  c.soff = p.tiled ? (static_cast<uint32_t>(wrow(sf, 0)) * static_cast<uint32_t>(ng) +
                       static_cast<uint32_t>(sizeof(ScaleT) == 4 ? lr : lr & ~1)) * sizeof(ScaleT)
-                   : static_cast<uint32_t>(wrow(lane >> 4, lr)) * static_cast<uint32_t>(ng) * sizeof(ScaleT);
+                   : static_cast<uint32_t>(wrow(sf, lr)) * static_cast<uint32_t>(ng) * sizeof(ScaleT);
 
   // source row of pass row r (rows past the pass repeat its last row)
   auto src_row = [&](int r) {
@@ -352,12 +367,12 @@ __device__ __forceinline__ void run_tile(const W4StreamParams& p, const TileLds&
   __syncthreads();  // the previous tile's readers are done with every LDS stage
 
   switch ((c.rows + 15) >> 4) {
-    case 1: tile_pass<kMode, ScaleT, 1>(p, lds, c); break;
-    case 2: tile_pass<kMode, ScaleT, 2>(p, lds, c); break;
-    case 3: tile_pass<kMode, ScaleT, 3>(p, lds, c); break;
-    case 4: tile_pass<kMode, ScaleT, 4>(p, lds, c); break;
-    case 5: tile_pass<kMode, ScaleT, 5>(p, lds, c); break;
-    default: tile_pass<kMode, ScaleT, 6>(p, lds, c); break;
+    case 1: tile_pass<kMode, ScaleT, 1, NF>(p, lds, c); break;
+    case 2: tile_pass<kMode, ScaleT, 2, NF>(p, lds, c); break;
+    case 3: tile_pass<kMode, ScaleT, 3, NF>(p, lds, c); break;
+    case 4: tile_pass<kMode, ScaleT, 4, NF>(p, lds, c); break;
+    case 5: tile_pass<kMode, ScaleT, 5, NF>(p, lds, c); break;
+    default: tile_pass<kMode, ScaleT, 6, NF>(p, lds, c); break;
   }
 }
 
@@ -378,23 +393,33 @@ __global__ __launch_bounds__(512) void w4_tile_kernel(W4StreamParams p) {
   // heaviest tiles first: the shared expert's full passes (the last passes of the table),
   // then the routed experts' in table order
   const int sp = p.has_shared ? (p.T + kTileM - 1) / kTileM : 0;
-  // Each workgroup takes its first tile by index, then asks a queue for more; every
-  // workgroup that ran a tile makes exactly one failing request, so the queue ends at
-  // `total` and the request that returns total - 1 is the launch's last: it resets the
+  // The tiles past the grid's last full round (when at most half a grid) run as two
+  // half-width pieces each: work items [0, full) are whole tiles, then two pieces per
+  // remaining tile.
+  const int grid = static_cast<int>(gridDim.x), rest = total % grid;
+  const int split = 2 * rest <= grid ? rest : 0;
+  const int full = total - split, items = full + 2 * split;
+  // Each workgroup takes its first item by index, then asks a queue for more; every
+  // workgroup that ran an item makes exactly one failing request, so the queue ends at
+  // `items` and the request that returns items - 1 is the launch's last: it resets the
   // queue for the next launch.  Nothing waits on the queue.
   int* queue = const_cast<int*>(p.meta) + (kMode == kModeGateUp ? 2 : 3);
 #ifdef DFLASH_TIMELINE
   int tl_n = 0;
 #endif
-  for (int tile = blockIdx.x; tile < total;) {
+  for (int item = blockIdx.x; item < items;) {
+    const bool whole = item < full;
+    const int tile = whole ? item : full + ((item - full) >> 1);
     const int i = tile / ntiles;
     const int P = i < sp ? passes - sp + i : i - sp;
+    const int nt = tile - i * ntiles;
 #ifdef DFLASH_TIMELINE
     unsigned long long* tl = g_timeline_tile +
         (((kMode == kModeGateUp ? 0 : 1) * kTlWorkgroups + blockIdx.x) * kTlTiles + min(tl_n, kTlTiles - 1)) * 3;
     if (threadIdx.x == 0 && blockIdx.x < kTlWorkgroups) tl[0] = __builtin_amdgcn_s_memrealtime();
 #endif
-    run_tile<kMode, ScaleT>(p, lds, P, tile - i * ntiles);
+    if (whole) run_tile<kMode, ScaleT, 4>(p, lds, P, nt);
+    else run_tile<kMode, ScaleT, 2>(p, lds, P, 2 * nt + ((item - full) & 1));
 #ifdef DFLASH_TIMELINE
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -402,17 +427,17 @@ __global__ __launch_bounds__(512) void w4_tile_kernel(W4StreamParams p) {
       const int4 d = ld_const_int4(p.pass_table, P);
       tl[1] = __builtin_amdgcn_s_memrealtime();
       tl[2] = static_cast<unsigned long long>(min(kTileM, d.z - d.w)) | (static_cast<unsigned long long>(P) << 16) |
-              (static_cast<unsigned long long>(tl_n + 1) << 40);
+              (static_cast<unsigned long long>(tl_n + 1) << 40) | (static_cast<unsigned long long>(whole ? 0 : 1) << 56);
     }
     ++tl_n;
 #endif
     if (threadIdx.x == 0) {
       const int got = __hip_atomic_fetch_add(queue, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (got == total - 1) __hip_atomic_store(queue, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      next_tile = static_cast<int>(gridDim.x) + got;
+      if (got == items - 1) __hip_atomic_store(queue, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      next_tile = grid + got;
     }
     __syncthreads();
-    tile = next_tile;
+    item = next_tile;
     __syncthreads();  // every wave has read next_tile before thread 0 may write it again
   }
 }
