@@ -440,35 +440,26 @@ __global__ __launch_bounds__(256) void route_count_kernel(RouteParams p) {
   if (lane_id() == 0) p.counts[e] = n;
 }
 
-// Exclusive prefix sum over the wave's lanes.
-__device__ __forceinline__ int wave_exclusive_scan(int v) {
-  const int lane = lane_id();
-  int incl = v;
-  for (int o = 1; o < 64; o <<= 1) {
-    const int u = __shfl_up(incl, o, 64);
-    if (lane >= o) incl += u;
-  }
-  return incl - v;
-}
-
 // grid = ceil(E/4), block = 256: one wave per expert writes its segment of the
 // permutation.  Lane l owns a contiguous run of the expert's slot-map row, so
 // an exclusive scan of the per-lane hit counts gives every token its position
-// in ascending token order.
+// in ascending token order.  The wave's loads go out before their first use (its
+// slot-map run, the counts of the experts below it, its own count), then the
+// routing weights of its first two chunks' pairs in one batch; sums and scans
+// are DPP reductions.
 __global__ __launch_bounds__(256) void route_permute_kernel(RouteParams p) {
   const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = lane_id();
   if (e >= p.E) return;
-  // this lane's run of the slot-map row (kept in registers for runs of up to 2 chunks), loaded
-  // before the count prefix so both latencies overlap
+  // this lane's run of the slot-map row (its first two chunks in registers)
   const int pitch = route_slot_pitch(p.T);
   const int per_lane = ((pitch >> 4) + 63) >> 6;  // 16-byte chunks per lane
   const uint4* row = reinterpret_cast<const uint4*>(p.slotmap + static_cast<int64_t>(e) * pitch);
   const int c0 = lane * per_lane, c1 = min(c0 + per_lane, pitch >> 4);
   const uint4 zero4 = make_uint4(0u, 0u, 0u, 0u);
   const uint4 r0 = c0 < c1 ? row[c0] : zero4, r1 = c0 + 1 < c1 ? row[c0 + 1] : zero4;
-  // the counts of the experts below e: every load in flight at once (a rolled loop waits for
-  // each before issuing the next); the resource reads 0 from e on
+  const int cnt = ld_const(p.counts, e);
+  // the counts of the experts below e (the resource reads 0 from e on)
   int before = 0, nz_before = 0, pass_before = 0;
   const buf_rsrc cr = make_rsrc(p.counts, static_cast<uint32_t>(e) * 4);
 #pragma unroll
@@ -478,10 +469,9 @@ __global__ __launch_bounds__(256) void route_permute_kernel(RouteParams p) {
     nz_before += c > 0 ? 1 : 0;
     pass_before += passes_for(c, p.rows_per_pass);
   }
-  before = wave_sum_int(before);
-  nz_before = wave_sum_int(nz_before);
-  pass_before = wave_sum_int(pass_before);
-  const int cnt = p.counts[e];
+  before = __builtin_amdgcn_readlane(wave_inclusive_scan(before), 63);
+  nz_before = __builtin_amdgcn_readlane(wave_inclusive_scan(nz_before), 63);
+  pass_before = __builtin_amdgcn_readlane(wave_inclusive_scan(pass_before), 63);
   if (lane == 0) {
     p.offsets[e] = before;
     if (cnt > 0) {
@@ -508,21 +498,22 @@ __global__ __launch_bounds__(256) void route_permute_kernel(RouteParams p) {
   if (cnt == 0) return;
   int mine = nonzero_bytes(r0) + nonzero_bytes(r1);
   for (int c = c0 + 2; c < c1; ++c) mine += nonzero_bytes(row[c]);
-  int pos = before + wave_exclusive_scan(mine);
-  // the routing weights of a chunk's pairs come in one batch of loads ahead of the writes
-  // (a load inside each pair's branch would wait once per byte position); empty bytes load
-  // past the end of the resource, which reads 0 without touching memory
+  int pos = before + wave_inclusive_scan(mine) - mine;
+  // the routing weights of a chunk's pairs come in one batch of loads ahead of the writes (a
+  // load inside each pair's branch would wait once per byte position); empty bytes load past
+  // the end of the resource, which reads 0 without touching memory
   const buf_rsrc wr = make_rsrc(p.wts, static_cast<uint32_t>(p.T * p.k) * 4);
-  for (int c = c0; c < c1 && mine > 0; ++c) {
-    const uint4 v = c == c0 ? r0 : c == c0 + 1 ? r1 : row[c];
+  auto chunk_weights = [&](const uint4& v, int c, float (&wt)[16]) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-    float wt[16];
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
       const int slot1 = (w[q >> 2] >> (8 * (q & 3))) & 0xFF;
       const uint32_t off = slot1 ? static_cast<uint32_t>(((16 * c + q) * p.k + slot1 - 1) * 4) : 0xFFFFFFF0u;
       wt[q] = buf_load_f32(wr, off, 0);
     }
+  };
+  auto chunk_write = [&](const uint4& v, int c, const float (&wt)[16]) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
       const int slot1 = (w[q >> 2] >> (8 * (q & 3))) & 0xFF;
@@ -534,9 +525,18 @@ __global__ __launch_bounds__(256) void route_permute_kernel(RouteParams p) {
         p.slot_w[pos] = wt[q];
         p.tok[pos] = t;
         ++pos;
-        --mine;
       }
     }
+  };
+  float w0[16], w1[16];
+  chunk_weights(r0, c0, w0);
+  chunk_weights(r1, c0 + 1, w1);
+  chunk_write(r0, c0, w0);
+  chunk_write(r1, c0 + 1, w1);
+  for (int c = c0 + 2; c < c1; ++c) {
+    const uint4 v = row[c];
+    chunk_weights(v, c, w0);
+    chunk_write(v, c, w0);
   }
 }
 // ---------------------------------------------------------------------------

@@ -165,6 +165,17 @@ __device__ __forceinline__ void topk2_any(const float* a, const float* b, bool l
   else wave_topk2<16>(a, b, live_b, E, k, id, w);
 }
 
+// Inclusive prefix sum over the 64 lanes (row shifts, then row broadcasts).
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 into rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 into rows 2, 3
+  return v;
+}
+
 __device__ __forceinline__ int passes_for(int rows, int rows_per_pass) {
   return (rows + rows_per_pass - 1) / rows_per_pass;
 }

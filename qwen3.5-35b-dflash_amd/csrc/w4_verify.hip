@@ -364,17 +364,6 @@ __device__ __forceinline__ float row_sum_f32(float v) {
   return v;
 }
 
-// Inclusive prefix sum over the 64 lanes (row shifts, then row broadcasts).
-__device__ __forceinline__ int wave_inclusive_scan(int v) {
-  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
-  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
-  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
-  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
-  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 into rows 1, 3
-  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 into rows 2, 3
-  return v;
-}
-
 // The keys of this lane's tokens (2 * wave + half-wave + 16 * pass); issued first
 // so the caller's staging loads queue behind them.
 template <int kPR>
