@@ -89,13 +89,16 @@ def test_router_logits(pkg, device, tokens):
 
 
 @pytest.mark.parametrize("tokens,experts,hidden", [
-    (100, 100, 1024), (65, 200, 768),
-    (300, 200, 512),      # 10 token tiles: one whole group of 8 and a partial group of 2
-    (64, 64, 2048),       # one partial group, one expert tile
-    (1000, 256, 1024),    # 32 token tiles, four whole groups, ragged last token tile
+    # 16 x 16 tiles (T < 1024, or H outside {512, 1024, 2048})
+    (100, 100, 1024), (65, 200, 768), (300, 200, 512), (64, 64, 2048), (1000, 256, 1024),
+    (1024, 64, 768),
+    # 32 x 64 tiles (T >= 1024, H in {512, 1024, 2048}), taken in groups of 8 token tiles
+    (1100, 200, 512),     # 35 token tiles (the last holds 12 rows): 4 whole groups and one of 3; 4 expert tiles (the last 8 experts)
+    (1030, 256, 1024),    # 33 token tiles (the last holds 6 rows): 4 whole groups and one of 1
+    (2048, 100, 2048),    # 64 token tiles in whole groups; 2 expert tiles (the last 36 experts)
 ])
 def test_router_logits_ragged_tiles(pkg, device, tokens, experts, hidden):
-    """Token and expert counts that leave partial 32 x 64 router tiles and partial tile groups."""
+    """Token and expert counts that leave partial router tiles and partial groups of token tiles."""
     print(f"router T={tokens} E={experts} H={hidden}", flush=True)
     gen = torch.Generator().manual_seed(tokens + experts)
     x = torch.randn((tokens, hidden), generator=gen).to(torch.bfloat16)
