@@ -68,6 +68,7 @@ struct TileLds {
   float* neg[kAStages];     // [128] -136*sum of each row's k-block (rows past the pass repeat the last)
   uint4* w[kWStages];       // [kWaves][4 fragments][64 lanes] packed weights
   uint32_t* s[kWStages];    // [kWaves][4 fragments x 16 columns] raw scale bits
+  float* wgt;               // [128] down: each pass row's routing weight (or shared-expert gate)
 };
 
 // Per-tile state shared by the subtile-count specialisations.
@@ -81,6 +82,8 @@ struct TileCtx {
   uint32_t soff;            // byte offset of the scale row this lane loads (fragment lane >> 4, column lane & 15)
   uint32_t aoff[3];         // byte offset of this lane's 16 bytes of activation blocks wave, wave + 8, wave + 16
   uint32_t noff;            // byte offset of the -136*sum terms of row 64 * wave + lane
+  buf_rsrc grs;             // down: the pass rows' routing weights (or shared-expert gates)
+  uint32_t goff;            // byte offset of the weight of row 64 * wave + lane
 };
 
 __device__ __forceinline__ void dma16(buf_rsrc r, void* dst, uint32_t voff, uint32_t soff) {
@@ -171,6 +174,9 @@ __device__ __forceinline__ void tile_pass(const W4StreamParams& p, const TileLds
   load_a(0, Idx<0>{});
   asm volatile("" ::: "memory");
   load_w(1, Idx<1>{});
+  // down: the rows' routing weights now, for the epilogue (loaded there, each row's weight
+  // would be a dependent memory round trip at the end of every tile)
+  if (kMode == kModeDown && wave * 64 < NSUB * 16) dma4(c.grs, lds.wgt + wave * 64, c.goff, 0);
 
   f32x4 u[NSUB][NF];  // running sums in units of the current k-block's scale
   float s_prev[NF], s_next[NF];
@@ -296,7 +302,7 @@ __device__ __forceinline__ void tile_pass(const W4StreamParams& p, const TileLds
         if (r >= c.rows) continue;
         const int m = d.w + r;
         const int yrow = c.shared ? p.T * p.top_k + m : d.y + m;
-        const float wgt = c.shared ? p.shared_gate[m] : p.slot_w[d.y + m];
+        const float wgt = lds.wgt[r];
         // weighted, in bf16: halves the y traffic of this launch and the combine's
         uint16_t* o = reinterpret_cast<uint16_t*>(p.out_f32) + static_cast<int64_t>(yrow) * p.N +
                       c.nt * kWaves * 16 * NF + wave * 16 * NF + lr;
@@ -365,6 +371,10 @@ __device__ __forceinline__ void run_tile(const W4StreamParams& p, const TileLds&
                 (4 * kq + (b & 3)) * 16;
   }
   c.noff = static_cast<uint32_t>(src_row(min(wave * 64 + lane, kTileM - 1))) * static_cast<uint32_t>(nkb) * 4;
+  if (kMode == kModeDown) {
+    c.grs = make_rsrc(c.shared ? p.shared_gate + c.d.w : p.slot_w + c.d.y + c.d.w, static_cast<uint32_t>(c.rows) * 4);
+    c.goff = static_cast<uint32_t>(min(wave * 64 + lane, c.rows - 1)) * 4;
+  }
 
   __syncthreads();  // the previous tile's readers are done with every LDS stage
 
@@ -384,10 +394,10 @@ template <int kMode, typename ScaleT>
 __global__ __launch_bounds__(512) void w4_tile_kernel(W4StreamParams p) {
   // the stages, a separate LDS array each
   __shared__ uint4 a0[kBlocks * 64], a1[kBlocks * 64];
-  __shared__ float n0[128], n1[128];
+  __shared__ float n0[128], n1[128], wg[128];
   __shared__ uint4 w0[kWaves * 4 * 64], w1[kWaves * 4 * 64], w2[kWaves * 4 * 64];
   __shared__ uint32_t s0[kWaves * 64], s1[kWaves * 64], s2[kWaves * 64];
-  const TileLds lds{{a0, a1}, {n0, n1}, {w0, w1, w2}, {s0, s1, s2}};
+  const TileLds lds{{a0, a1}, {n0, n1}, {w0, w1, w2}, {s0, s1, s2}, wg};
   __shared__ int next_tile;
   const int ntiles = p.strips;  // column tiles per pass
   const int passes = ld_const(p.meta, 1);
