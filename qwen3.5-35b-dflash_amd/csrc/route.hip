@@ -440,13 +440,20 @@ __global__ __launch_bounds__(256) void route_count_kernel(RouteParams p) {
   if (lane_id() == 0) p.counts[e] = n;
 }
 
+// Pairs up to which route_permute counts the experts itself (from the selected ids) and the
+// count launch is skipped.
+constexpr int kPermuteCountPairs = 2048;
+
 // grid = ceil(E/4), block = 256: one wave per expert writes its segment of the
 // permutation.  Lane l owns a contiguous run of the expert's slot-map row, so
 // an exclusive scan of the per-lane hit counts gives every token its position
 // in ascending token order.  The wave's loads go out before their first use (its
 // slot-map run, the counts of the experts below it, its own count), then the
 // routing weights of its first two chunks' pairs in one batch; sums and scans
-// are DPP reductions.
+// are DPP reductions.  kCount (T*k <= kPermuteCountPairs): every wave builds the
+// expert histogram of all T*k selected ids in its own LDS row (one 16-byte load
+// per lane per 1024 ids, LDS atomic adds), in place of route_count's launch.
+template <bool kCount>
 __global__ __launch_bounds__(256) void route_permute_kernel(RouteParams p) {
   const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = lane_id();
@@ -458,16 +465,41 @@ __global__ __launch_bounds__(256) void route_permute_kernel(RouteParams p) {
   const int c0 = lane * per_lane, c1 = min(c0 + per_lane, pitch >> 4);
   const uint4 zero4 = make_uint4(0u, 0u, 0u, 0u);
   const uint4 r0 = c0 < c1 ? row[c0] : zero4, r1 = c0 + 1 < c1 ? row[c0 + 1] : zero4;
-  const int cnt = ld_const(p.counts, e);
-  // the counts of the experts below e (the resource reads 0 from e on)
-  int before = 0, nz_before = 0, pass_before = 0;
-  const buf_rsrc cr = make_rsrc(p.counts, static_cast<uint32_t>(e) * 4);
+  int cnt = 0, before = 0, nz_before = 0, pass_before = 0;
+  if constexpr (kCount) {
+    __shared__ int hist[4][kMaxExperts];
+    int* h = hist[threadIdx.x >> 6];
+    for (int i = lane; i < p.E; i += 64) h[i] = 0;
+    const int n = p.T * p.k;
+    const buf_rsrc ir = make_rsrc(p.ids, static_cast<uint32_t>(n) * 4);
+    uint4 v[kPermuteCountPairs / 256];
 #pragma unroll
-  for (int j = 0; j < kMaxExperts / 64; ++j) {
-    const int c = static_cast<int>(__float_as_uint(buf_load_f32(cr, static_cast<uint32_t>(lane + 64 * j) * 4, 0)));
-    before += c;
-    nz_before += c > 0 ? 1 : 0;
-    pass_before += passes_for(c, p.rows_per_pass);
+    for (int j = 0; j < kPermuteCountPairs / 256; ++j) v[j] = buf_load16(ir, static_cast<uint32_t>(lane + 64 * j) * 16, 0);
+#pragma unroll
+    for (int j = 0; j < kPermuteCountPairs / 256; ++j) {
+      const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (4 * (lane + 64 * j) + q < n) atomicAdd(&h[w[q]], 1);
+    }
+    cnt = h[e];
+    for (int e2 = lane; e2 < e; e2 += 64) {
+      const int c = h[e2];
+      before += c;
+      nz_before += c > 0 ? 1 : 0;
+      pass_before += passes_for(c, p.rows_per_pass);
+    }
+  } else {
+    cnt = ld_const(p.counts, e);
+    // the counts of the experts below e (the resource reads 0 from e on)
+    const buf_rsrc cr = make_rsrc(p.counts, static_cast<uint32_t>(e) * 4);
+#pragma unroll
+    for (int j = 0; j < kMaxExperts / 64; ++j) {
+      const int c = static_cast<int>(__float_as_uint(buf_load_f32(cr, static_cast<uint32_t>(lane + 64 * j) * 4, 0)));
+      before += c;
+      nz_before += c > 0 ? 1 : 0;
+      pass_before += passes_for(c, p.rows_per_pass);
+    }
   }
   before = __builtin_amdgcn_readlane(wave_inclusive_scan(before), 63);
   nz_before = __builtin_amdgcn_readlane(wave_inclusive_scan(nz_before), 63);
@@ -709,8 +741,12 @@ void launch_route(const RouteParams& p, bool zeroed, hipStream_t stream) {
                        reinterpret_cast<uint32_t*>(p.counts), words);
   }
   if (p.T > 0) hipLaunchKernelGGL(route_topk_kernel, dim3((p.T + 3) / 4), dim3(256), 0, stream, p);
+  if (static_cast<int64_t>(p.T) * p.k <= kPermuteCountPairs && reinterpret_cast<uintptr_t>(p.ids) % 16 == 0) {
+    hipLaunchKernelGGL(route_permute_kernel<true>, dim3((p.E + 3) / 4), dim3(256), 0, stream, p);
+    return;
+  }
   hipLaunchKernelGGL(route_count_kernel, dim3((p.E + 3) / 4), dim3(256), 0, stream, p);
-  hipLaunchKernelGGL(route_permute_kernel, dim3((p.E + 3) / 4), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL(route_permute_kernel<false>, dim3((p.E + 3) / 4), dim3(256), 0, stream, p);
 }
 
 void launch_table_prep(const TableParams& p, hipStream_t stream) {
