@@ -441,8 +441,8 @@ __global__ __launch_bounds__(256) void route_count_kernel(RouteParams p) {
 }
 
 // Pairs up to which route_permute counts the experts itself (from the selected ids) and the
-// count launch is skipped.
-constexpr int kPermuteCountPairs = 2048;
+// count launch is skipped: each of a workgroup's 256 threads loads up to 16 x 4 ids.
+constexpr int kPermuteCountPairs = 16384;
 
 // grid = ceil(E/4), block = 256: one wave per expert writes its segment of the
 // permutation.  Lane l owns a contiguous run of the expert's slot-map row, so
@@ -450,13 +450,33 @@ constexpr int kPermuteCountPairs = 2048;
 // in ascending token order.  The wave's loads go out before their first use (its
 // slot-map run, the counts of the experts below it, its own count), then the
 // routing weights of its first two chunks' pairs in one batch; sums and scans
-// are DPP reductions.  kCount (T*k <= kPermuteCountPairs): every wave builds the
-// expert histogram of all T*k selected ids in its own LDS row (one 16-byte load
-// per lane per 1024 ids, LDS atomic adds), in place of route_count's launch.
+// are DPP reductions.  kCount (T*k <= kPermuteCountPairs): every workgroup builds
+// the expert histogram of all T*k selected ids in LDS (one 16-byte load per thread
+// per 1024 ids, LDS atomic adds), in place of route_count's launch.
 template <bool kCount>
 __global__ __launch_bounds__(256) void route_permute_kernel(RouteParams p) {
   const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = lane_id();
+  __shared__ int hist[kCount ? kMaxExperts : 1];
+  if constexpr (kCount) {  // every thread of the workgroup takes part, live expert or not
+    for (int i = threadIdx.x; i < p.E; i += 256) hist[i] = 0;
+    __syncthreads();
+    const int n = p.T * p.k;
+    const buf_rsrc ir = make_rsrc(p.ids, static_cast<uint32_t>(n) * 4);
+    uint4 v[kPermuteCountPairs / 1024];
+#pragma unroll
+    for (int j = 0; j < kPermuteCountPairs / 1024; ++j)
+      v[j] = 4 * (threadIdx.x + 256 * j) < n ? buf_load16(ir, static_cast<uint32_t>(threadIdx.x + 256 * j) * 16, 0)
+                                             : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+    for (int j = 0; j < kPermuteCountPairs / 1024; ++j) {
+      const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (4 * (threadIdx.x + 256 * j) + q < n) atomicAdd(&hist[w[q]], 1);
+    }
+    __syncthreads();
+  }
   if (e >= p.E) return;
   // this lane's run of the slot-map row (its first two chunks in registers)
   const int pitch = route_slot_pitch(p.T);
@@ -467,24 +487,9 @@ __global__ __launch_bounds__(256) void route_permute_kernel(RouteParams p) {
   const uint4 r0 = c0 < c1 ? row[c0] : zero4, r1 = c0 + 1 < c1 ? row[c0 + 1] : zero4;
   int cnt = 0, before = 0, nz_before = 0, pass_before = 0;
   if constexpr (kCount) {
-    __shared__ int hist[4][kMaxExperts];
-    int* h = hist[threadIdx.x >> 6];
-    for (int i = lane; i < p.E; i += 64) h[i] = 0;
-    const int n = p.T * p.k;
-    const buf_rsrc ir = make_rsrc(p.ids, static_cast<uint32_t>(n) * 4);
-    uint4 v[kPermuteCountPairs / 256];
-#pragma unroll
-    for (int j = 0; j < kPermuteCountPairs / 256; ++j) v[j] = buf_load16(ir, static_cast<uint32_t>(lane + 64 * j) * 16, 0);
-#pragma unroll
-    for (int j = 0; j < kPermuteCountPairs / 256; ++j) {
-      const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (4 * (lane + 64 * j) + q < n) atomicAdd(&h[w[q]], 1);
-    }
-    cnt = h[e];
+    cnt = hist[e];
     for (int e2 = lane; e2 < e; e2 += 64) {
-      const int c = h[e2];
+      const int c = hist[e2];
       before += c;
       nz_before += c > 0 ? 1 : 0;
       pass_before += passes_for(c, p.rows_per_pass);
