@@ -49,9 +49,10 @@ def test_route_golden_vectors(pkg, device):
 
 
 @pytest.mark.parametrize("tokens,experts,k", [
-    (1, 256, 8), (16, 256, 8), (128, 256, 8), (256, 256, 8),     # single-workgroup path (T*k <= 2048)
-    (257, 256, 8), (2048, 256, 8),                                # multi-workgroup path
+    (1, 256, 8), (16, 256, 8), (32, 256, 8),                      # single-workgroup path (T <= 32)
+    (128, 256, 8), (256, 256, 8), (257, 256, 8), (2048, 256, 8),  # multi-workgroup, experts counted in the permutation launch
     (64, 1024, 64), (300, 1000, 3), (40, 7, 7), (33, 64, 1),
+    (2100, 256, 8), (4096, 64, 6),                                # T*k > 16384: the separate count launch
 ])
 def test_route_random(pkg, device, tokens, experts, k):
     print(f"route T={tokens} E={experts} k={k}", flush=True)
