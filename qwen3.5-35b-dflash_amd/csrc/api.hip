@@ -586,7 +586,7 @@ int run_experts(const MoeShapes& S, const int32_t* inv, void* ws, const MoeLayou
 
 dflash::RouteParams route_params(const float* logits, int64_t T, int64_t E, int64_t k, int32_t* ids, float* wts,
                                  int32_t* perm, int32_t* inv, int32_t* offsets, void* ws, const RouteLayout& L,
-                                 int rows_per_pass, bool shared) {
+                                 int rows_per_pass, bool shared, bool sort_passes = false) {
   dflash::RouteParams r{};
   r.logits = logits;
   r.T = static_cast<int>(T);
@@ -609,6 +609,7 @@ dflash::RouteParams route_params(const float* logits, int64_t T, int64_t E, int6
   r.tok = at<int32_t>(ws, L.tok);
   r.rows_per_pass = rows_per_pass;
   r.has_shared = shared ? 1 : 0;
+  r.sort_passes = sort_passes ? 1 : 0;
   return r;
 }
 
@@ -946,8 +947,10 @@ static int moe_w4a16_body(const void* hidden, int64_t tokens, int64_t hidden_siz
     if (!measuring()) dflash::launch_front(f, st);
     if (int r = launch_status("front")) return r;
     if (!(verify && vgu.route)) {
+      // the prefill tile kernels take the routed passes longest first
       const dflash::RouteParams r = route_params(logits, S.T, S.E, S.k, topk_ids, topk_weights, perm, inv_perm,
-                                                 expert_offsets, workspace, L.route, rows_per_pass(S), S.shared);
+                                                 expert_offsets, workspace, L.route, rows_per_pass(S), S.shared,
+                                                 !verify && moe_gemm_path(S) == GemmPath::kTile);
       if (!measuring()) dflash::launch_route(r, true, st);
       if (int rc = launch_status("route")) return rc;
     }

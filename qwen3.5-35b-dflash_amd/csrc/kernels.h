@@ -54,6 +54,10 @@ struct RouteParams {
   int32_t* tok;         // [T*k] token of every slot row (perm[i] / k)
   int rows_per_pass;
   int has_shared;
+  // prefill tile path (route_permute only): the routed experts' passes go into pass_table in
+  // descending order of 16-row subtiles, the order in which the tile kernels' queue hands
+  // them out (longest first); pass_slot is then not written for them
+  int sort_passes;
 };
 
 struct TableParams {

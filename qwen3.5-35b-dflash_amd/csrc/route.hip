@@ -440,6 +440,16 @@ __global__ __launch_bounds__(256) void route_count_kernel(RouteParams p) {
   if (lane_id() == 0) p.counts[e] = n;
 }
 
+// Buckets of the sorted pass table: an expert with c rows has c / rows_per_pass full passes and
+// a last pass of the remaining rows; bucket j holds the passes of rows_per_pass / 16 - j
+// 16-row subtiles.  n0: the expert's passes in bucket 0 (its full passes, and its last pass when
+// that has as many subtiles); jl: the bucket of a lighter last pass, or -1.
+__device__ __forceinline__ void pass_buckets(int c, int rows_per_pass, int& n0, int& jl) {
+  const int full = c / rows_per_pass, sub = (c - full * rows_per_pass + 15) >> 4, top = rows_per_pass >> 4;
+  n0 = full + (sub == top ? 1 : 0);
+  jl = sub > 0 && sub < top ? top - sub : -1;
+}
+
 // Pairs up to which route_permute counts the experts itself (from the selected ids) and the
 // count launch is skipped: each of a workgroup's 256 threads loads up to 16 x 4 ids.
 constexpr int kPermuteCountPairs = 16384;
@@ -452,7 +462,10 @@ constexpr int kPermuteCountPairs = 16384;
 // routing weights of its first two chunks' pairs in one batch; sums and scans
 // are DPP reductions.  kCount (T*k <= kPermuteCountPairs): every workgroup builds
 // the expert histogram of all T*k selected ids in LDS (one 16-byte load per thread
-// per 1024 ids, LDS atomic adds), in place of route_count's launch.
+// per 1024 ids, LDS atomic adds), in place of route_count's launch.  sort_passes: the
+// wave also reads the counts of the experts above it and places each of its passes at its rank
+// in descending subtile order (passes of heavier buckets anywhere, then those of its own
+// bucket in lower experts).
 template <bool kCount>
 __global__ __launch_bounds__(256) void route_permute_kernel(RouteParams p) {
   const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -485,36 +498,61 @@ __global__ __launch_bounds__(256) void route_permute_kernel(RouteParams p) {
   const int c0 = lane * per_lane, c1 = min(c0 + per_lane, pitch >> 4);
   const uint4 zero4 = make_uint4(0u, 0u, 0u, 0u);
   const uint4 r0 = c0 < c1 ? row[c0] : zero4, r1 = c0 + 1 < c1 ? row[c0 + 1] : zero4;
-  int cnt = 0, before = 0, nz_before = 0, pass_before = 0;
+  const int cnt = kCount ? hist[e] : ld_const(p.counts, e);
+  // sorted pass table: this expert's passes of the heaviest bucket (full ones, and a last pass
+  // of as many subtiles), and the bucket of its lighter last pass (-1: none)
+  int own0 = 0, jl = -1;
+  if (p.sort_passes) pass_buckets(cnt, p.rows_per_pass, own0, jl);
+  // sums over the experts below e; sorted table: the heaviest-bucket passes below e, the passes
+  // in jl below e, and the passes of every expert in buckets heavier than jl
+  int before = 0, nz_before = 0, pass_before = 0, pre0 = 0, prel = 0, heavier = 0;
+  auto add = [&](int e2, int c) {
+    if (e2 < e) {
+      before += c;
+      nz_before += c > 0 ? 1 : 0;
+      pass_before += passes_for(c, p.rows_per_pass);
+    }
+    if (p.sort_passes) {
+      int n0, j;
+      pass_buckets(c, p.rows_per_pass, n0, j);
+      if (e2 < e) {
+        pre0 += n0;
+        prel += j == jl ? 1 : 0;
+      }
+      heavier += (jl > 0 ? n0 : 0) + (j >= 0 && j < jl ? 1 : 0);
+    }
+  };
+  const int span = p.sort_passes ? p.E : e;  // experts whose counts are read
   if constexpr (kCount) {
-    cnt = hist[e];
-    for (int e2 = lane; e2 < e; e2 += 64) {
-      const int c = hist[e2];
-      before += c;
-      nz_before += c > 0 ? 1 : 0;
-      pass_before += passes_for(c, p.rows_per_pass);
-    }
+    for (int e2 = lane; e2 < span; e2 += 64) add(e2, hist[e2]);
   } else {
-    cnt = ld_const(p.counts, e);
-    // the counts of the experts below e (the resource reads 0 from e on)
-    const buf_rsrc cr = make_rsrc(p.counts, static_cast<uint32_t>(e) * 4);
+    // the resource reads 0 from span on
+    const buf_rsrc cr = make_rsrc(p.counts, static_cast<uint32_t>(span) * 4);
 #pragma unroll
-    for (int j = 0; j < kMaxExperts / 64; ++j) {
-      const int c = static_cast<int>(__float_as_uint(buf_load_f32(cr, static_cast<uint32_t>(lane + 64 * j) * 4, 0)));
-      before += c;
-      nz_before += c > 0 ? 1 : 0;
-      pass_before += passes_for(c, p.rows_per_pass);
-    }
+    for (int j = 0; j < kMaxExperts / 64; ++j)
+      add(lane + 64 * j,
+          static_cast<int>(__float_as_uint(buf_load_f32(cr, static_cast<uint32_t>(lane + 64 * j) * 4, 0))));
   }
   before = __builtin_amdgcn_readlane(wave_inclusive_scan(before), 63);
   nz_before = __builtin_amdgcn_readlane(wave_inclusive_scan(nz_before), 63);
   pass_before = __builtin_amdgcn_readlane(wave_inclusive_scan(pass_before), 63);
+  if (p.sort_passes) {
+    pre0 = __builtin_amdgcn_readlane(wave_inclusive_scan(pre0), 63);
+    prel = __builtin_amdgcn_readlane(wave_inclusive_scan(prel), 63);
+    heavier = __builtin_amdgcn_readlane(wave_inclusive_scan(heavier), 63);
+  }
   if (lane == 0) {
     p.offsets[e] = before;
     if (cnt > 0) {
       p.hit[nz_before] = e;
       p.pass_start[nz_before] = pass_before;
-      write_slot(p.slot_table, p.pass_slot, p.pass_table, nz_before, e, before, cnt, pass_before, p.rows_per_pass);
+      if (p.sort_passes) {
+        p.slot_table[nz_before] = make_int4(e, before, cnt, pass_before);
+        for (int i = 0; i < own0; ++i) p.pass_table[pre0 + i] = make_int4(e, before, cnt, i * p.rows_per_pass);
+        if (jl >= 0) p.pass_table[heavier + prel] = make_int4(e, before, cnt, own0 * p.rows_per_pass);
+      } else {
+        write_slot(p.slot_table, p.pass_slot, p.pass_table, nz_before, e, before, cnt, pass_before, p.rows_per_pass);
+      }
     }
     if (e == p.E - 1) {
       const int nh = nz_before + (cnt > 0 ? 1 : 0);

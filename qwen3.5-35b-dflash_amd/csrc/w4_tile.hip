@@ -2,10 +2,13 @@
 //
 // A work tile is one pass (up to 96 rows of one slot: an expert segment or
 // the shared expert) times one column tile of 512 outputs; persistent
-// workgroups (one per CU, 8 waves, 64 columns each) take tiles round robin.
-// The tiles left over after the last full round of the grid run as two
-// half-width pieces each (8 waves, 32 columns each), so that final round
-// spreads over twice as many workgroups.
+// workgroups (one per CU, 8 waves, 64 columns each) take tiles from a queue,
+// longest passes first (the routing writes the routed passes in descending
+// order of 16-row subtiles).  The tiles left over after the last full round of
+// the grid run in pieces, so that final round spreads over more workgroups:
+// four per tile (two half-width column pieces of 8 waves x 32 columns, each
+// over the first and the second half of the pass's subtiles) when they fill at
+// most a quarter of the grid, else two half-width pieces when at most half.
 // Per 128-column k-block of the reduction:
 //   * every operand reaches LDS by direct-to-LDS buffer loads (no register
 //     staging): the pass's activation rows in MFMA fragment order (1 KB
@@ -46,7 +49,7 @@ constexpr int kTileM = 96;                  // rows per pass (6 subtiles of 16)
 // Per-tile times of the profiling build (DFLASH_TIMELINE, loaded only by timeline.py): per
 // launch mode (gate/up, down), workgroup and its first 8 tiles, s_memrealtime ticks (100 MHz)
 // at the tile's start and end and the tile's rows | pass << 16 | (order + 1) << 40 | half << 56
-// (1 for a half-width piece).
+// (1 for a piece of a split tile; rows are the whole pass's).
 #ifdef DFLASH_TIMELINE
 constexpr int kTlWorkgroups = 1024, kTlTiles = 8;
 __device__ unsigned long long g_timeline_tile[2 * kTlWorkgroups * kTlTiles * 3];
@@ -315,8 +318,9 @@ __device__ __forceinline__ void tile_pass(const W4StreamParams& p, const TileLds
 
 // One work tile: pass P (up to 96 rows of one slot) times column tile nt of 8 x 16 NF columns
 // (gate/up: 8 x 8 NF of each half).
+// rhalf: 0 for every row of the pass, 1 for its first ceil(nsub / 2) subtiles, 2 for the rest.
 template <int kMode, typename ScaleT, int NF>
-__device__ __forceinline__ void run_tile(const W4StreamParams& p, const TileLds& lds, int P, int nt) {
+__device__ __forceinline__ void run_tile(const W4StreamParams& p, const TileLds& lds, int P, int nt, int rhalf) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = lane_id(), lr = lane & 15, kq = lane >> 4;
@@ -339,6 +343,16 @@ __device__ __forceinline__ void run_tile(const W4StreamParams& p, const TileLds&
   c.d = ld_const_int4(p.pass_table, P);
   c.shared = c.d.x < 0;
   c.rows = min(kTileM, c.d.z - c.d.w);
+  if (rhalf) {
+    const int lo = 16 * ((((c.rows + 15) >> 4) + 1) >> 1);
+    if (rhalf == 2) {
+      c.d.w += lo;
+      c.rows -= lo;
+    } else {
+      c.rows = min(c.rows, lo);
+    }
+    if (c.rows <= 0) return;  // a one-subtile pass has no second half
+  }
   c.ars = make_rsrc(p.act, act_rows * static_cast<uint32_t>(K) * 2);
   c.nrs = make_rsrc(p.act_neg, act_rows * static_cast<uint32_t>(nkb) * 4);
   c.wrs = make_rsrc(c.shared ? p.w_shared : p.w + static_cast<int64_t>(c.d.x) * p.w_stride,
@@ -402,15 +416,17 @@ __global__ __launch_bounds__(512) void w4_tile_kernel(W4StreamParams p) {
   const int ntiles = p.strips;  // column tiles per pass
   const int passes = ld_const(p.meta, 1);
   const int total = passes * ntiles;
-  // heaviest tiles first: the shared expert's full passes (the last passes of the table),
-  // then the routed experts' in table order
+  // heaviest tiles first: the shared expert's passes (the last passes of the table), then the
+  // routed experts' in table order (descending subtile count on this path)
   const int sp = p.has_shared ? (p.T + kTileM - 1) / kTileM : 0;
-  // The tiles past the grid's last full round (when at most half a grid) run as two
-  // half-width pieces each: work items [0, full) are whole tiles, then two pieces per
-  // remaining tile.
+  // The tiles past the grid's last full round run in pieces (4 when they fill at most a
+  // quarter of the grid, 2 when at most half): work items [0, full) are whole tiles, then
+  // `pieces` per remaining tile (piece q: half-width column piece q & 1, row half q >> 1 when
+  // there are 4).  A row half with no rows (one-subtile pass) is an empty item.
   const int grid = static_cast<int>(gridDim.x), rest = total % grid;
-  const int split = 2 * rest <= grid ? rest : 0;
-  const int full = total - split, items = full + 2 * split;
+  const int pieces = 4 * rest <= grid ? 4 : 2 * rest <= grid ? 2 : 1;
+  const int split = pieces > 1 ? rest : 0;
+  const int full = total - split, items = full + pieces * split;
   // Each workgroup takes its first item by index, then asks a queue for more; every
   // workgroup that ran an item makes exactly one failing request, so the queue ends at
   // `items` and the request that returns items - 1 is the launch's last: it resets the
@@ -421,7 +437,8 @@ __global__ __launch_bounds__(512) void w4_tile_kernel(W4StreamParams p) {
 #endif
   for (int item = blockIdx.x; item < items;) {
     const bool whole = item < full;
-    const int tile = whole ? item : full + ((item - full) >> 1);
+    const int q = whole ? 0 : (item - full) & (pieces - 1);
+    const int tile = whole ? item : full + (item - full) / pieces;
     const int i = tile / ntiles;
     const int P = i < sp ? passes - sp + i : i - sp;
     const int nt = tile - i * ntiles;
@@ -430,8 +447,8 @@ __global__ __launch_bounds__(512) void w4_tile_kernel(W4StreamParams p) {
         (((kMode == kModeGateUp ? 0 : 1) * kTlWorkgroups + blockIdx.x) * kTlTiles + min(tl_n, kTlTiles - 1)) * 3;
     if (threadIdx.x == 0 && blockIdx.x < kTlWorkgroups) tl[0] = __builtin_amdgcn_s_memrealtime();
 #endif
-    if (whole) run_tile<kMode, ScaleT, 4>(p, lds, P, nt);
-    else run_tile<kMode, ScaleT, 2>(p, lds, P, 2 * nt + ((item - full) & 1));
+    if (whole) run_tile<kMode, ScaleT, 4>(p, lds, P, nt, 0);
+    else run_tile<kMode, ScaleT, 2>(p, lds, P, 2 * nt + (q & 1), pieces == 4 ? 1 + (q >> 1) : 0);
 #ifdef DFLASH_TIMELINE
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();

@@ -11,9 +11,10 @@ markdown:
   launches): per phase the spread over workgroups of its time since the
   launch's first workgroup started, and per wave the median time its k-loop
   ended (waves w and w + 4 share a SIMD);
-* T=2048 prefill, gate/up and down tile launches: tiles per workgroup, the
-  spread of workgroup end times, and the median tile duration by 16-row
-  subtile count.
+* T=2048 prefill, gate/up and down tile launches: work items per workgroup,
+  the spread of workgroup end times, the median whole-tile duration by 16-row
+  subtile count, and the count and median duration of the pieces the last
+  tiles are split into.
 
 The timestamps come from thread 0 (lane 0 of each wave for the k-loop ends)
 after the workgroup's own stores have completed; they include the cost of the
@@ -138,17 +139,25 @@ def tile_report(lib, pkg, device, reps: int) -> list[str]:
             s["per_wg"].extend(used[wgs].sum(axis=1).tolist())
             s["wg_end"].extend((np.where(used, en, 0).max(axis=1)[wgs] - t0).tolist())
             rows = t[m, :, :, 2] & 0xFFFF
-            for sub, d in zip(((rows[used] + 15) // 16).tolist(), (en - st)[used].tolist()):
+            piece = used & (((t[m, :, :, 2] >> 56) & 1) == 1)
+            whole = used & ~piece
+            for sub, d in zip(((rows[whole] + 15) // 16).tolist(), (en - st)[whole].tolist()):
                 s[f"sub{sub}"].append(d)
+            s["pieces"].append(int(piece.sum()))
+            s["piece_us"].extend((en - st)[piece].tolist())
     for name, s in stats.items():
         hist = np.bincount(s["per_wg"])
-        out += [f"**{name} launch**: {s['tiles'][0]} tiles, span {np.median(s['span']) / 100:.1f} us (median of calls)",
-                "", f"- tiles per workgroup (count of workgroups, over calls): "
+        pieces = s["pieces"][0]
+        out += [f"**{name} launch**: {s['tiles'][0]} work items ({s['tiles'][0] - pieces} whole tiles, {pieces} "
+                f"pieces of split tiles), span {np.median(s['span']) / 100:.1f} us (median of calls)",
+                "", f"- work items per workgroup (count of workgroups, over calls): "
                 f"{ {i: int(c) for i, c in enumerate(hist) if c} }",
                 f"- workgroup end (us): min | median | p90 | max = {_spread(s['wg_end'])}",
-                "- median tile duration by 16-row subtiles (us): " +
+                "- median whole-tile duration by 16-row subtiles (us): " +
                 ", ".join(f"{k[3:]}: {np.median(v) / 100:.1f} ({len(v) // reps} tiles)"
-                          for k, v in sorted(s.items()) if k.startswith("sub")), ""]
+                          for k, v in sorted(s.items()) if k.startswith("sub")),
+                f"- pieces: median {np.median(s['piece_us']) / 100 if s['piece_us'] else 0:.1f} us, "
+                f"max {max(s['piece_us'], default=0) / 100:.1f} us", ""]
     return out
 
 
