@@ -175,57 +175,88 @@ __device__ __forceinline__ void router_tile(const uint16_t* __restrict__ x, cons
   }
 }
 
-// Router logits for a 32-token x 64-expert tile (long T).  The 8 waves split H: wave w
-// takes the 32-column k-steps w, w + 8, w + 16, ... (the eight waves of a step read 512
-// contiguous bytes of every row), loads every A and B fragment of its steps straight from
-// global memory into registers, all of them in flight at once, and accumulates a partial
-// 32 x 64 tile; the partials meet in LDS and are summed in wave order.
+// Router logits for a 32-token x 64-expert tile (long T), read in whole cache lines.  The
+// tile's 96 rows (32 token rows of x, then 64 expert rows of W) are read in chunks of 256
+// columns: wave instruction q of a chunk reads 512 contiguous bytes of rows 2q and 2q + 1
+// (loads that cover only half of each 128-byte line, as MFMA fragments read straight from
+// memory do, stream about a third as fast per CU), and every load of the tile is in flight
+// at once (kSteps chunks x 6 per lane).  Each chunk passes through LDS, row-major with its
+// 16-byte slots XOR-swizzled by row & 7 so that the fragment reads are free of bank
+// conflicts.  Wave w accumulates a 32 x 32 block (both token subtiles, expert subtiles
+// 2 (w & 1) and 2 (w & 1) + 1) over k-steps 2 (w >> 1) and 2 (w >> 1) + 1 of every chunk, one
+// fragment read per MFMA; the four waves of an expert half then add their partials through LDS
+// in k-step order.
 template <int kSteps>
-__device__ __forceinline__ void router_split_tile(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-                                                  float* __restrict__ logits, int T, int E, int t0, int e0,
-                                                  f32x4 (*red)[8][64]) {
+__device__ __forceinline__ void router_line_tile(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                 float* __restrict__ logits, int T, int E, int t0, int e0,
+                                                 uint4* stage_u4) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // a plain vector: stays in registers
   constexpr int H = kSteps * 256;
   const int wave = threadIdx.x >> 6, lane = lane_id(), lr = lane & 15, kq = lane >> 4;
-  const uint16_t* xa[2];
-  const uint16_t* wb[4];
+  u32x4* stage = reinterpret_cast<u32x4*>(stage_u4);
+  const u32x4* src[6];
+  int dst[6];  // slot of the loaded 16 bytes in the chunk's LDS copy (32 slots per row)
 #pragma unroll
-  for (int ts = 0; ts < 2; ++ts)
-    xa[ts] = x + static_cast<int64_t>(min(t0 + 16 * ts + lr, T - 1)) * H + wave * 32 + kq * 8;
-#pragma unroll
-  for (int es = 0; es < 4; ++es)
-    wb[es] = w + static_cast<int64_t>(min(e0 + 16 * es + lr, E - 1)) * H + wave * 32 + kq * 8;
-  uint4 a[kSteps][2], b[kSteps][4];
-#pragma unroll
-  for (int s = 0; s < kSteps; ++s) {
-#pragma unroll
-    for (int ts = 0; ts < 2; ++ts) a[s][ts] = *reinterpret_cast<const uint4*>(xa[ts] + s * 256);
-#pragma unroll
-    for (int es = 0; es < 4; ++es) b[s][es] = *reinterpret_cast<const uint4*>(wb[es] + s * 256);
+  for (int j = 0; j < 6; ++j) {
+    const int r = 2 * (6 * wave + j) + (lane >> 5);  // tile row 0..95
+    const uint16_t* row = r < 32 ? x + static_cast<int64_t>(min(t0 + r, T - 1)) * H
+                                 : w + static_cast<int64_t>(min(e0 + r - 32, E - 1)) * H;
+    src[j] = reinterpret_cast<const u32x4*>(row) + (lane & 31);
+    dst[j] = r * 32 + ((lane & 31) ^ (r & 7));
   }
-  // every load goes out before the first MFMA waits (the scheduler would otherwise sink
-  // loads between the MFMAs and wait for each soon after issuing it)
+  u32x4 v[kSteps][6];
+#pragma unroll
+  for (int c = 0; c < kSteps; ++c)
+#pragma unroll
+    for (int j = 0; j < 6; ++j) v[c][j] = src[j][32 * c];
+  // every load goes out before the first one is waited for
   __builtin_amdgcn_sched_barrier(0);
-  f32x4 acc[2][4];
+  // wave w: expert half w & 1 (subtiles 2 (w & 1) and 2 (w & 1) + 1), k-steps 2 (w >> 1) and
+  // 2 (w >> 1) + 1 of every chunk, both token subtiles
+  const int eh = wave & 1, kp = wave >> 1;
+  f32x4 acc[2][2];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) acc[j >> 2][j & 3] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < 4; ++i) acc[i >> 1][i & 1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  static_for(std::make_integer_sequence<int, kSteps>{}, [&](auto ci) {
+    constexpr int c = decltype(ci)::value;
 #pragma unroll
-  for (int s = 0; s < kSteps; ++s)
+    for (int j = 0; j < 6; ++j) stage[dst[j]] = v[c][j];
+    lds_barrier();  // the chunk is in LDS (the later chunks' loads stay in flight)
 #pragma unroll
-    for (int ts = 0; ts < 2; ++ts)
+    for (int h = 0; h < 2; ++h) {
+      const int s = 2 * kp + h;
+      u32x4 a[2], b[2];
 #pragma unroll
-      for (int es = 0; es < 4; ++es) acc[ts][es] = mfma16x16x32(a[s][ts], b[s][es], acc[ts][es]);
+      for (int ts = 0; ts < 2; ++ts) {
+        const int ra = 16 * ts + lr;
+        a[ts] = stage[ra * 32 + ((4 * s + kq) ^ (ra & 7))];
+      }
 #pragma unroll
-  for (int j = 0; j < 8; ++j) red[wave][j][lane] = acc[j >> 2][j & 3];
-  __syncthreads();
-  // thread (j, lane) sums block j = (token subtile, expert subtile) of the eight partials
-  const int j = wave;
-  f32x4 sum = red[0][j][lane];
+      for (int el = 0; el < 2; ++el) {
+        const int rb = 32 + 16 * (2 * eh + el) + lr;
+        b[el] = stage[rb * 32 + ((4 * s + kq) ^ (rb & 7))];
+      }
 #pragma unroll
-  for (int v = 1; v < 8; ++v) sum += red[v][j][lane];
-  const int e = e0 + 16 * (j & 3) + lr;
+      for (int i = 0; i < 4; ++i)
+        acc[i >> 1][i & 1] = mfma16x16x32(__builtin_bit_cast(uint4, a[i >> 1]), __builtin_bit_cast(uint4, b[i & 1]),
+                                          acc[i >> 1][i & 1]);
+    }
+    lds_barrier();  // every wave has read the chunk before the next one is written (or the partials)
+  });
+  // partials: red[wave][subtile (ts, el)][lane]; then wave w sums subtile (w >> 2, w & 3) over the
+  // four k-step pairs in order
+  f32x4* red = reinterpret_cast<f32x4*>(stage_u4);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 64 + lane] = acc[i >> 1][i & 1];
+  lds_barrier();
+  const int ts = wave >> 2, es = wave & 3, i_sub = ts * 2 + (es & 1);
+  f32x4 sum = red[(((0 << 1) | (es >> 1)) * 4 + i_sub) * 64 + lane];
+#pragma unroll
+  for (int q = 1; q < 4; ++q) sum += red[(((q << 1) | (es >> 1)) * 4 + i_sub) * 64 + lane];
+  const int e = e0 + 16 * es + lr;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int t = t0 + 16 * (j >> 2) + 4 * kq + i;
+    const int t = t0 + 16 * ts + 4 * kq + i;
     if (t < T && e < E) logits[static_cast<int64_t>(t) * E + e] = sum[i];
   }
 }
@@ -254,7 +285,7 @@ __global__ __launch_bounds__(512) void front_kernel(FrontParams p) {
   }
   b -= p.n_zero;
   if (p.router_big) {
-    __shared__ f32x4 red[8][8][64];  // one buffer for every H instance
+    __shared__ uint4 stage[96 * 32];  // one 256-column chunk of the tile's 96 rows, every H instance
     // the expert tiles of a token tile share its rows: blocks b, b + 8, ... of a group of
     // 8 token tiles take them (consecutive workgroups go to different XCDs, each with its L2)
     const int tiles_e = (p.E + 63) / 64, tiles_t = (p.T + 31) / 32;
@@ -262,9 +293,9 @@ __global__ __launch_bounds__(512) void front_kernel(FrontParams p) {
     const bool whole = group * 8 + 8 <= tiles_t;
     const int tt = group * 8 + (whole ? r % 8 : r / tiles_e), te = whole ? r / 8 : r % tiles_e;
     const int t0 = tt * 32, e0 = te * 64;
-    if (p.H == 512) router_split_tile<2>(p.x, p.router_w, p.logits, p.T, p.E, t0, e0, red);
-    else if (p.H == 1024) router_split_tile<4>(p.x, p.router_w, p.logits, p.T, p.E, t0, e0, red);
-    else router_split_tile<8>(p.x, p.router_w, p.logits, p.T, p.E, t0, e0, red);
+    if (p.H == 512) router_line_tile<2>(p.x, p.router_w, p.logits, p.T, p.E, t0, e0, stage);
+    else if (p.H == 1024) router_line_tile<4>(p.x, p.router_w, p.logits, p.T, p.E, t0, e0, stage);
+    else router_line_tile<8>(p.x, p.router_w, p.logits, p.T, p.E, t0, e0, stage);
   } else {
     const int tiles_e = (p.E + 15) / 16;
     router_tile(p.x, p.router_w, p.logits, p.T, p.E, p.H, (b / tiles_e) * 16, (b % tiles_e) * 16);
