@@ -136,7 +136,8 @@ __device__ __forceinline__ void prep_block(const uint16_t* __restrict__ x, int K
 }
 
 // Router logits for a 16x16 tile: fp32 [T][E] = x bf16 [T][H] . W bf16 [E][H]^T;
-// 8 waves split H (H % 256 == 0) and are reduced through LDS.
+// 8 waves split H (H % 256 == 0) and are reduced through LDS.  Used for hidden sizes other
+// than 512, 1024 and 2048, which take the whole-line tiles below.
 __device__ __forceinline__ void router_tile(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                             float* __restrict__ logits, int T, int E, int H, int t0, int e0) {
   __shared__ f32x4 red[8][64];
@@ -171,6 +172,65 @@ __device__ __forceinline__ void router_tile(const uint16_t* __restrict__ x, cons
     for (int i = 0; i < 4; ++i) {
       const int t = t0 + 4 * kq + i;
       if (t < T && e < E) logits[static_cast<int64_t>(t) * E + e] = s[i];
+    }
+  }
+}
+
+// Router logits for a 16-token x 16-expert tile, read in whole cache lines (short T at
+// H in {512, 1024, 2048}): the tile's 32 rows (16 token rows of x, then 16 expert rows of W)
+// in chunks of 256 columns, wave instruction j of a chunk reading 512 contiguous bytes of rows
+// 4 wave + 2 j and 4 wave + 2 j + 1, every load in flight at once; each chunk passes through
+// an LDS copy with XOR-swizzled 16-byte slots, wave w takes k-step w of every chunk, and the
+// eight partial tiles are added through LDS in wave order.
+template <int kSteps>
+__device__ __forceinline__ void router_line_tile16(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                   float* __restrict__ logits, int T, int E, int t0, int e0,
+                                                   uint4* stage_u4) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // a plain vector: stays in registers
+  constexpr int H = kSteps * 256;
+  const int wave = threadIdx.x >> 6, lane = lane_id(), lr = lane & 15, kq = lane >> 4;
+  u32x4* stage = reinterpret_cast<u32x4*>(stage_u4);
+  const u32x4* src[2];
+  int dst[2];  // slot of the loaded 16 bytes in the chunk's LDS copy (32 slots per row)
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int r = 4 * wave + 2 * j + (lane >> 5);  // tile row 0..31
+    const uint16_t* row = r < 16 ? x + static_cast<int64_t>(min(t0 + r, T - 1)) * H
+                                 : w + static_cast<int64_t>(min(e0 + r - 16, E - 1)) * H;
+    src[j] = reinterpret_cast<const u32x4*>(row) + (lane & 31);
+    dst[j] = r * 32 + ((lane & 31) ^ (r & 7));
+  }
+  u32x4 v[kSteps][2];
+#pragma unroll
+  for (int c = 0; c < kSteps; ++c)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) v[c][j] = src[j][32 * c];
+  // every load goes out before the first one is waited for
+  __builtin_amdgcn_sched_barrier(0);
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const int slot = 4 * wave + kq;  // k-step wave of the chunk, this lane's 8 columns
+  static_for(std::make_integer_sequence<int, kSteps>{}, [&](auto ci) {
+    constexpr int c = decltype(ci)::value;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) stage[dst[j]] = v[c][j];
+    lds_barrier();  // the chunk is in LDS (the later chunks' loads stay in flight)
+    const u32x4 a = stage[lr * 32 + (slot ^ (lr & 7))];
+    const u32x4 b = stage[(16 + lr) * 32 + (slot ^ (lr & 7))];
+    acc = mfma16x16x32(__builtin_bit_cast(uint4, a), __builtin_bit_cast(uint4, b), acc);
+    lds_barrier();  // every wave has read the chunk before the next one is written (or the partials)
+  });
+  f32x4* red = reinterpret_cast<f32x4*>(stage_u4);
+  red[wave * 64 + lane] = acc;
+  lds_barrier();
+  if (wave == 0) {
+    f32x4 sum = red[lane];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) sum += red[i * 64 + lane];
+    const int e = e0 + lr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = t0 + 4 * kq + i;
+      if (t < T && e < E) logits[static_cast<int64_t>(t) * E + e] = sum[i];
     }
   }
 }
@@ -284,8 +344,8 @@ __global__ __launch_bounds__(512) void front_kernel(FrontParams p) {
     return;
   }
   b -= p.n_zero;
+  __shared__ uint4 stage[96 * 32];  // whole-line router tiles: one 256-column chunk of the tile's rows
   if (p.router_big) {
-    __shared__ uint4 stage[96 * 32];  // one 256-column chunk of the tile's 96 rows, every H instance
     // the expert tiles of a token tile share its rows: blocks b, b + 8, ... of a group of
     // 8 token tiles take them (consecutive workgroups go to different XCDs, each with its L2)
     const int tiles_e = (p.E + 63) / 64, tiles_t = (p.T + 31) / 32;
@@ -298,7 +358,11 @@ __global__ __launch_bounds__(512) void front_kernel(FrontParams p) {
     else router_line_tile<8>(p.x, p.router_w, p.logits, p.T, p.E, t0, e0, stage);
   } else {
     const int tiles_e = (p.E + 15) / 16;
-    router_tile(p.x, p.router_w, p.logits, p.T, p.E, p.H, (b / tiles_e) * 16, (b % tiles_e) * 16);
+    const int t0 = (b / tiles_e) * 16, e0 = (b % tiles_e) * 16;
+    if (p.H == 512) router_line_tile16<2>(p.x, p.router_w, p.logits, p.T, p.E, t0, e0, stage);
+    else if (p.H == 1024) router_line_tile16<4>(p.x, p.router_w, p.logits, p.T, p.E, t0, e0, stage);
+    else if (p.H == 2048) router_line_tile16<8>(p.x, p.router_w, p.logits, p.T, p.E, t0, e0, stage);
+    else router_tile(p.x, p.router_w, p.logits, p.T, p.E, p.H, t0, e0);
   }
 }
 
