@@ -930,7 +930,10 @@ static int moe_w4a16_body(const void* hidden, int64_t tokens, int64_t hidden_siz
     f.H = static_cast<int>(S.H);
     f.router_big = dflash::router_big_fits(T, f.H) ? 1 : 0;
     f.n_router = router_logits ? 0 : dflash::router_tiles(T, E, f.H);
-    f.prep_rows = T;
+    // with multi-workgroup routing the activation prep runs in the route_topk launch instead
+    const bool route_launch = !(verify && vgu.route);
+    const bool prep_in_route = route_launch && !small && T > 0;
+    f.prep_rows = prep_in_route ? 0 : T;
     f.x_il = at<uint16_t>(workspace, L.x_il);
     f.xneg = at<float>(workspace, L.xneg);
     f.gate_w = S.shared ? static_cast<const uint16_t*>(shared_gate_weight) : nullptr;
@@ -946,11 +949,20 @@ static int moe_w4a16_body(const void* hidden, int64_t tokens, int64_t hidden_siz
     }
     if (!measuring()) dflash::launch_front(f, st);
     if (int r = launch_status("front")) return r;
-    if (!(verify && vgu.route)) {
+    if (route_launch) {
       // the prefill tile kernels take the routed passes longest first
-      const dflash::RouteParams r = route_params(logits, S.T, S.E, S.k, topk_ids, topk_weights, perm, inv_perm,
+      dflash::RouteParams r = route_params(logits, S.T, S.E, S.k, topk_ids, topk_weights, perm, inv_perm,
                                                  expert_offsets, workspace, L.route, rows_per_pass(S), S.shared,
                                                  !verify && moe_gemm_path(S) == GemmPath::kTile);
+      if (prep_in_route) {
+        r.prep_x = f.x;
+        r.prep_H = f.H;
+        r.prep_rows = T;
+        r.prep_x_il = f.x_il;
+        r.prep_xneg = f.xneg;
+        r.prep_gate_w = f.gate_w;
+        r.prep_gate_out = f.gate_out;
+      }
       if (!measuring()) dflash::launch_route(r, true, st);
       if (int rc = launch_status("route")) return rc;
     }

@@ -58,6 +58,15 @@ struct RouteParams {
   // descending order of 16-row subtiles, the order in which the tile kernels' queue hands
   // them out (longest first); pass_slot is then not written for them
   int sort_passes;
+  // activation prep by extra blocks of the route_topk launch (multi-workgroup routing only,
+  // prep_rows > 0): rows of x converted as front_kernel's prep blocks would, while the routing
+  // runs (no routing kernel reads them)
+  const uint16_t* prep_x;
+  uint16_t* prep_x_il;
+  float* prep_xneg;
+  const uint16_t* prep_gate_w;
+  float* prep_gate_out;
+  int prep_H, prep_rows;
 };
 
 struct TableParams {

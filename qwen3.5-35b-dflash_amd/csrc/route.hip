@@ -73,7 +73,7 @@ __device__ __forceinline__ void prep_row(const uint16_t* __restrict__ x, int K, 
     gate_acc = wave_sum(gate_acc);
     if (lane_id() == 0 && tid < 256) part[tid >> 6] = gate_acc;
     __syncthreads();
-    if (tid == 0) gate_out[row] = 1.0f / (1.0f + __expf(-(part[0] + part[1] + part[2] + part[3])));
+    if (tid == 0) gate_out[row] = 1.0f / (1.0f + __expf(-((part[0] + part[1]) + (part[2] + part[3]))));
   }
 }
 
@@ -500,6 +500,11 @@ __global__ void route_zero_kernel(uint32_t* __restrict__ words, int64_t n) {
 
 // grid = ceil(T/4), block = 256: one wave per token.
 __global__ __launch_bounds__(256) void route_topk_kernel(RouteParams p) {
+  const int topk_blocks = (p.T + 3) >> 2;
+  if (static_cast<int>(blockIdx.x) >= topk_blocks) {  // prep blocks: one row each
+    prep_row(p.prep_x, p.prep_H, blockIdx.x - topk_blocks, p.prep_x_il, p.prep_xneg, p.prep_gate_w, p.prep_gate_out);
+    return;
+  }
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = lane_id();
   if (t >= p.T) return;
@@ -878,7 +883,7 @@ void launch_route(const RouteParams& p, bool zeroed, hipStream_t stream) {
     hipLaunchKernelGGL(route_zero_kernel, dim3(blocks), dim3(256), 0, stream,
                        reinterpret_cast<uint32_t*>(p.counts), words);
   }
-  if (p.T > 0) hipLaunchKernelGGL(route_topk_kernel, dim3((p.T + 3) / 4), dim3(256), 0, stream, p);
+  if (p.T > 0) hipLaunchKernelGGL(route_topk_kernel, dim3((p.T + 3) / 4 + p.prep_rows), dim3(256), 0, stream, p);
   if (static_cast<int64_t>(p.T) * p.k <= kPermuteCountPairs && reinterpret_cast<uintptr_t>(p.ids) % 16 == 0) {
     hipLaunchKernelGGL(route_permute_kernel<true>, dim3((p.E + 3) / 4), dim3(256), 0, stream, p);
     return;
