@@ -24,7 +24,7 @@ struct FrontParams {
   int T, E, H;
   int n_router;             // router tiles (0 when the logits are given)
   int router_big;           // 32 x 64 tiles (router_big_fits) instead of 16 x 16
-  int prep_rows;            // rows of x to prepare (T, or 0 for router tiles only)
+  int prep_rows;            // rows of x to prepare (T, or 0: router tiles only, or the prep runs in route_topk's launch)
   uint16_t* x_il;           // octet-interleaved copy of x [T][H]
   float* xneg;              // -136 * sum per 128-column block [T][H/128]
   const uint16_t* gate_w;   // shared-expert gate vector [H] or null
