@@ -147,6 +147,7 @@ def test_routing_from_hidden_matches_oracle_logits(pkg, device, tokens, seed):
     (9, 8, 8, 512, 512, 128, torch.bfloat16, True),           # small-T kernel, E == k
     (300, 16, 4, 1024, 512, 128, torch.float32, True),        # tiled prefill kernel, fp32 scales
     (256, 8, 2, 2048, 512, 256, torch.bfloat16, False),       # tiled prefill kernel, group 256
+    (2100, 64, 8, 512, 512, 128, torch.bfloat16, True),       # tiled prefill kernel past 16384 pairs: count launch, sorted passes
     (16, 256, 8, 2048, 512, 256, torch.float32, True),        # verify kernels, the reference quantizer's g256 fp32
     (5, 8, 2, 512, 512, 256, torch.bfloat16, False),          # verify kernels, group 256, K = 512 (one group per 2 k-blocks)
     (32, 64, 8, 2048, 1024, 256, torch.float32, True),        # verify kernels at their largest T, group 256
