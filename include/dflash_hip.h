@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DFLASH_ABI_VERSION 4
+#define DFLASH_ABI_VERSION 5
 
 enum dflash_status {
   DFLASH_OK = 0,
@@ -113,6 +113,17 @@ const char* dflash_last_error(void);
 size_t dflash_qlinear_workspace_bytes(int64_t m, int64_t k, int64_t group_size);
 int dflash_qlinear_w4a16(const void* x, int64_t m, const dflash_w4* weight, void* y, void* workspace,
                          size_t workspace_bytes, void* stream);
+
+/*
+ * The same qlinear with y fp32 [m][N]: the fp32 sums, not rounded.  For a packed
+ * router (the gate.weight key is linear_int4 in the portable plan,
+ * graph/quant_plan.py:25-32), whose logits feed the top-k: the vendor path ranks
+ * the QuantMatmul output (fused/quantization.py:183-184); here routing stays a
+ * function of the unrounded fp32 logits, so it is bit-exact against a CPU top-k
+ * of the same logits.  Same constraints and workspace as dflash_qlinear_w4a16.
+ */
+int dflash_qlinear_w4a16_f32(const void* x, int64_t m, const dflash_w4* weight, float* y, void* workspace,
+                             size_t workspace_bytes, void* stream);
 
 /*
  * Router logits, fp32 [tokens][experts] = hidden bf16 [tokens][H] . router_weight bf16 [E][H]^T,

@@ -12,7 +12,7 @@ from pathlib import Path
 PACKAGE_DIR = Path(__file__).resolve().parent
 LIBRARY_PATH = PACKAGE_DIR / "libdflash_hip.so"
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 DTYPE_BF16 = 0
 DTYPE_F32 = 1
 DTYPE_F16 = 2
@@ -57,6 +57,7 @@ SIGNATURES = {
     "dflash_last_error": (ctypes.c_char_p, []),
     "dflash_qlinear_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
     "dflash_qlinear_w4a16": (ctypes.c_int, [_P, _I64, _W4P, _P, _P, _SZ, _P]),
+    "dflash_qlinear_w4a16_f32": (ctypes.c_int, [_P, _I64, _W4P, _P, _P, _SZ, _P]),
     "dflash_router_logits": (ctypes.c_int, [_P, _I64, _I64, _P, _I64, _P, _P]),
     "dflash_moe_route_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
     "dflash_moe_route": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _SZ, _P]),

@@ -689,8 +689,10 @@ size_t dflash_qlinear_workspace_bytes(int64_t m, int64_t k, int64_t group_size) 
   return c.off;
 }
 
-int dflash_qlinear_w4a16(const void* x, int64_t m, const dflash_w4* weight, void* y, void* workspace,
-                         size_t workspace_bytes, void* stream) {
+namespace {
+// Both qlinear entry points: y is bf16 [m][N], or fp32 when y_f32.
+int qlinear_impl(const void* x, int64_t m, const dflash_w4* weight, void* y, bool y_f32, void* workspace,
+                 size_t workspace_bytes, void* stream) {
   try {
     if (!weight) return fail(DFLASH_ERR_INVALID_ARGUMENT, "weight descriptor is NULL");
     if (m < 0) return fail(DFLASH_ERR_INVALID_ARGUMENT, "m must be >= 0");
@@ -741,7 +743,8 @@ int dflash_qlinear_w4a16(const void* x, int64_t m, const dflash_w4* weight, void
     p.act = x_il;
     p.act_neg = xneg;
     p.neg_parts = 1;
-    p.out_bf16 = static_cast<uint16_t*>(y);
+    p.out_bf16 = y_f32 ? nullptr : static_cast<uint16_t*>(y);
+    p.out_f32 = y_f32 ? static_cast<float*>(y) : nullptr;
     p.M = static_cast<int>(m);
     if (verify) {
       p.act_neg = nullptr;
@@ -749,7 +752,8 @@ int dflash_qlinear_w4a16(const void* x, int64_t m, const dflash_w4* weight, void
       p.strips = p.N / 32;
       for (int64_t r0 = 0; r0 < m; r0 += vrows) {
         p.act = static_cast<const uint16_t*>(x) + r0 * K;
-        p.out_bf16 = static_cast<uint16_t*>(y) + r0 * N;
+        if (y_f32) p.out_f32 = static_cast<float*>(y) + r0 * N;
+        else p.out_bf16 = static_cast<uint16_t*>(y) + r0 * N;
         p.M = static_cast<int>(std::min(vrows, m - r0));
         vl.g = p;
         dflash::launch_w4_verify(dflash::kModeLinear, weight->scale_dtype == DFLASH_DTYPE_F32, cu_count(), vl, st);
@@ -765,6 +769,17 @@ int dflash_qlinear_w4a16(const void* x, int64_t m, const dflash_w4* weight, void
   } catch (...) {
     return fail(DFLASH_ERR_HIP, "unexpected host exception");
   }
+}
+}  // namespace
+
+int dflash_qlinear_w4a16(const void* x, int64_t m, const dflash_w4* weight, void* y, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  return qlinear_impl(x, m, weight, y, false, workspace, workspace_bytes, stream);
+}
+
+int dflash_qlinear_w4a16_f32(const void* x, int64_t m, const dflash_w4* weight, float* y, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  return qlinear_impl(x, m, weight, y, true, workspace, workspace_bytes, stream);
 }
 
 int dflash_router_logits(const void* hidden, int64_t tokens, int64_t hidden_size, const void* router_weight,

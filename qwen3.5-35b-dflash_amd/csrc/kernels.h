@@ -132,7 +132,8 @@ struct W4StreamParams {
   // outputs
   uint16_t* out_bf16;      // kModeLinear: [M][N]; kModeGateUp: h [(T*k+T)][N/2] interleaved
   float* out_part;         // kModeGateUp: [(T*k+T)][N/32] partial -136*sum(h) per 16 columns ([N/256] per 128 on the tile kernel)
-  float* out_f32;          // kModeDown: y [(T*k+T)][N] (the tile kernel writes it as bf16)
+  float* out_f32;          // kModeDown: y [(T*k+T)][N] (the tile kernel writes it as bf16);
+                           // kModeLinear: when set, y [M][N] in fp32 instead of out_bf16
   const float* slot_w;     // kModeDown: routing weight of every slot row [T*k]
   const float* shared_gate;// kModeDown: sigmoid gate [T]
   int M;                   // kModeLinear rows

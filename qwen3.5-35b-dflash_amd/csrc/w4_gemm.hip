@@ -120,7 +120,11 @@ __device__ __forceinline__ void w4_pass(const W4StreamParams& p, const uint8_t* 
       const int m = m0 + mt * 16 + 4 * kq + e;
       const bool valid = m < M;
       if (kMode == kModeLinear) {
-        if (valid) {
+        if (valid && p.out_f32) {  // fp32 output: the unrounded sums
+          float* o = p.out_f32 + static_cast<int64_t>(m) * p.N;
+          o[row0 + lr] = tot0[mt][e];
+          o[row1 + lr] = tot1[mt][e];
+        } else if (valid) {
           uint16_t* o = p.out_bf16 + static_cast<int64_t>(m) * p.N;
           o[row0 + lr] = f32_to_bf16(tot0[mt][e]);
           o[row1 + lr] = f32_to_bf16(tot1[mt][e]);

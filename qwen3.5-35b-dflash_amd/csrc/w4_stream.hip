@@ -325,7 +325,11 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(W4StreamParams p) {
           const int m = m0 + mt * 16 + 4 * kq + e;
           const bool valid = m < cd.M;
           if (kMode == kModeLinear) {
-            if (valid) {
+            if (valid && p.out_f32) {  // fp32 output: the unrounded sums
+              float* o = p.out_f32 + static_cast<int64_t>(m) * p.N + row0 + lr;
+              o[0] = v0;
+              o[second] = v1;
+            } else if (valid) {
               uint16_t* o = p.out_bf16 + static_cast<int64_t>(m) * p.N + row0 + lr;
               o[0] = f32_to_bf16(v0);
               o[second] = f32_to_bf16(v1);

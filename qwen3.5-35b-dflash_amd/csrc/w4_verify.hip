@@ -767,7 +767,11 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
         const int m = m0 + 4 * kq + e;
         const bool valid = m < M;
         if (kMode == kModeLinear) {
-          if (valid) {
+          if (valid && p.out_f32) {  // fp32 output: the unrounded sums
+            float* o = p.out_f32 + static_cast<int64_t>(m) * p.N + row0 + lr;
+            o[0] = t0[e];
+            o[16] = t1[e];
+          } else if (valid) {
             uint16_t* o = p.out_bf16 + static_cast<int64_t>(m) * p.N + row0 + lr;
             o[0] = f32_to_bf16(t0[e]);
             o[16] = f32_to_bf16(t1[e]);

@@ -119,22 +119,26 @@ def to_tiled(w: PackedW4) -> PackedW4:
     return PackedW4(packed, scales, w.group_size, "tiled")
 
 
-def qlinear(x: torch.Tensor, weight: PackedW4, *, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """W4A16 linear ``x[..., K] -> [..., N]`` (bf16 in, bf16 out, fp32 accumulation)."""
+def qlinear(x: torch.Tensor, weight: PackedW4, *, workspace: Optional[torch.Tensor] = None,
+            out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """W4A16 linear ``x[..., K] -> [..., N]`` (bf16 in, fp32 accumulation; bf16 out, or the
+    unrounded fp32 sums with ``out_dtype=torch.float32``)."""
     weight.validate("weight")
     if weight.packed.ndim != 2:
         raise ValueError("qlinear takes one packed matrix [N, K/2]")
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("qlinear writes bfloat16 or float32")
     device = _require_device(x, weight.packed)
     if x.dtype != torch.bfloat16 or x.shape[-1] != weight.cols:
         raise ValueError(f"x must be bfloat16 [..., {weight.cols}]")
     flat = x.reshape(-1, weight.cols).contiguous()
     m = flat.shape[0]
-    out = torch.empty((m, weight.rows), dtype=torch.bfloat16, device=device)
+    out = torch.empty((m, weight.rows), dtype=out_dtype, device=device)
     lib = _lib.load()
     ws = _workspace(lib.dflash_qlinear_workspace_bytes(m, weight.cols, weight.group_size), device, workspace)
     desc = _desc(weight)
-    _lib.call("dflash_qlinear_w4a16", _ptr(flat), m, ctypes.byref(desc), _ptr(out), _ptr(ws), ws.numel(),
-              _stream(device))
+    entry = "dflash_qlinear_w4a16_f32" if out_dtype == torch.float32 else "dflash_qlinear_w4a16"
+    _lib.call(entry, _ptr(flat), m, ctypes.byref(desc), _ptr(out), _ptr(ws), ws.numel(), _stream(device))
     return out.reshape(*x.shape[:-1], weight.rows)
 
 

@@ -95,11 +95,12 @@ class QuantizedWeights(torch.nn.Module):
         return out.to(torch.float16).reshape(*x.shape[:-1], bank.rows)
 
     def router_logits(self, flat: Tensor, key: str) -> Tensor:
-        """fp32 logits ``[T, E]``: the bf16 router's exact-fp32 GEMV, or a packed router's qlinear."""
+        """fp32 logits ``[T, E]``: the bf16 router's GEMV, or a packed router's qlinear, both the
+        unrounded fp32 sums, so the top-k ranks exact logits (no bf16 ties at the k-th place)."""
         if key in self._routers:
             return ops.router_logits(flat, self._routers[key])
         if key in self._banks:
-            return ops.qlinear(flat, self._banks[key]).float()
+            return ops.qlinear(flat, self._banks[key], out_dtype=torch.float32)
         raise ValueError(f"invalid original quant linear invocation: {key}")
 
     def moe(self, x: Tensor, prefix: str, *, top_k: int) -> Tensor:

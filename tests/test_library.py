@@ -28,7 +28,15 @@ def test_library_loads_and_exports_every_symbol(pkg):
     lib = pkg._lib.load()
     for name in _declared_functions():
         assert hasattr(lib, name), name
-    assert lib.dflash_abi_version() == pkg._lib.ABI_VERSION == 4
+    header_abi = int(re.search(r"#define DFLASH_ABI_VERSION (\d+)", HEADER.read_text()).group(1))
+    assert lib.dflash_abi_version() == pkg._lib.ABI_VERSION == header_abi
+
+
+def test_integration_binding_asserts_the_current_abi():
+    """The reference-side ctypes stub in INTEGRATION.md checks the ABI the header declares."""
+    header_abi = int(re.search(r"#define DFLASH_ABI_VERSION (\d+)", HEADER.read_text()).group(1))
+    stub = re.findall(r"dflash_abi_version\(\) == (\d+)", (ROOT / "INTEGRATION.md").read_text())
+    assert stub and all(int(v) == header_abi for v in stub), stub
 
 
 def test_library_has_no_unresolved_internal_symbols(pkg):
@@ -64,6 +72,22 @@ def _desc(pkg, experts=1, rows=512, cols=2048, group=128, dtype=0, packed=16, sc
 def _status(pkg, name, *args):
     lib = pkg._lib.load()
     return getattr(lib, name)(*args), lib.dflash_last_error().decode()
+
+
+@host_only
+def test_qlinear_f32_validation(pkg):
+    ws = ctypes.c_void_p(4096)
+    st, msg = _status(pkg, "dflash_qlinear_w4a16_f32", ctypes.c_void_p(16), 16, None, ctypes.c_void_p(16), ws,
+                      1 << 20, None)
+    assert st == 1 and "NULL" in msg
+    d = _desc(pkg, rows=48)
+    st, msg = _status(pkg, "dflash_qlinear_w4a16_f32", ctypes.c_void_p(16), 16, ctypes.byref(d),
+                      ctypes.c_void_p(16), ws, 1 << 20, None)
+    assert st == 2 and "N % 32" in msg
+    d = _desc(pkg)
+    st, msg = _status(pkg, "dflash_qlinear_w4a16_f32", ctypes.c_void_p(16), 16, ctypes.byref(d),
+                      ctypes.c_void_p(16), ws, 16, None)
+    assert st == 3 and "workspace" in msg
 
 
 @host_only

@@ -126,3 +126,46 @@ def test_adapter_linear_and_moe_on_the_kernels(pkg, device):
     rep = metrics.compare(composed.reshape(16, -1).float().cpu(), fused.float().cpu())
     print(f"  composed vs fused shared expert: {rep}", flush=True)
     assert rep["max_rel"] <= 2e-2 and rep["cosine"] > 0.999
+
+
+@pytest.mark.gpu
+def test_packed_router_routes_on_unrounded_logits(pkg, device):
+    """A packed int4 router (``linear_int4`` in the portable plan): its logits come from the
+    fp32-output qlinear, unrounded, and the layer's routing is bit-exact against the oracle's
+    top-k and permutation of those very logits (``fused/quantization.py:183-192``)."""
+    from oracle import moe as oracle_moe, routing as oracle_routing, w4 as oracle_w4
+    c = pkg.target.small_config()
+    c = type(c)(**{**vars(c), "linear_value_heads": 32, "experts": 32})   # router rows: qlinear N % 32
+    w = pkg.target.random_weights(c, seed=5, device=device, layout="portable")
+    q0 = pkg.quantized.from_target_weights(w, layout="portable")
+    key = "target.layers.0.mlp.gate.weight"
+    gen = torch.Generator().manual_seed(6)
+    router = pkg.synthetic.int4_weight(gen, (c.experts, c.hidden))
+    banks = dict(q0._banks)
+    banks[key] = pkg.PackedW4(router.packed.to(device), router.scales.to(device), router.group_size)
+    routers = {k: v for k, v in q0._routers.items() if k != key}
+    q = pkg.quantized.QuantizedWeights(q0.shapes, banks, (w.embedding, w.embedding_scale), routers=routers)
+    x = torch.randn((1, 16, c.hidden), generator=gen).to(device)
+    xb = x.reshape(16, -1).to(torch.bfloat16)
+    logits = q.router_logits(xb, key)
+    assert logits.dtype == torch.float32
+    ref_logits = oracle_w4.qlinear(xb.cpu(), router.packed.numpy(), router.scales, 128)
+    ref_logits = torch.as_tensor(ref_logits, dtype=torch.float64)
+    err = (logits.double().cpu() - ref_logits).abs().max() / ref_logits.abs().max()
+    assert err < 1e-5, err                                             # fp32 sums, not a bf16 rounding
+    assert not torch.equal(logits, logits.to(torch.bfloat16).float())
+    lw = w.layers[0]
+    gu, dn = lw.gate_up.tiled(), lw.down.tiled()
+    out, r, used = pkg.ops.moe_w4a16(xb, gu, dn, top_k=c.top_k, router_logits=logits, return_routing=True)
+    ids, wts = oracle_routing.topk(used.cpu().numpy(), c.top_k)
+    perm, inv, offsets = oracle_routing.permutation(ids, c.experts)
+    assert torch.equal(r.ids.cpu(), torch.from_numpy(ids))
+    assert torch.equal(r.perm.cpu(), torch.from_numpy(perm)) and torch.equal(r.inv.cpu(), torch.from_numpy(inv))
+    assert torch.equal(r.offsets.cpu(), torch.from_numpy(offsets))
+    torch.testing.assert_close(r.weights.cpu(), torch.from_numpy(wts), rtol=2e-6, atol=2e-6)
+    routed = q.moe(x, "target.layers.0.mlp", top_k=c.top_k)
+    assert torch.equal(routed.reshape(16, -1), out.to(torch.float16))
+    golden = oracle_moe.moe(xb.cpu(), logits.cpu().numpy(), c.top_k, (lw.gate_up.packed.cpu(), lw.gate_up.scales.cpu()),
+                            (lw.down.packed.cpu(), lw.down.scales.cpu()), 128)
+    rep = metrics.compare(out.cpu(), golden["out_f32"])
+    assert rep["max_rel"] <= metrics.MAX_REL_TOLERANCE, rep
