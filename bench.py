@@ -12,17 +12,20 @@ multi-layer verify forward would be issued), so host launch overhead is not
 part of the measurement.
 
 Prints ONE JSON line.  ``value`` is microseconds per MoE layer (lower is
-better).  ``roofline`` is the dominant kernel, the grouped gate/up launch as it
-runs in the layer (it routes the block in its prologue, from the step's router
-logits, then streams the hit experts' gate/up rows): HIP events on its launch
-stream bracket graph replays that hold only that kernel's launches
-(measurement mode of the library), one per step over the same rotation of
-weight sets and hidden blocks; achieved = its algorithmic bytes (int4 gate/up
-rows + bf16 scales of the hit experts and the shared expert, x in, h out) /
-mean launch duration.  ``traffic`` is the HBM bytes the same kernel moves per
-launch, from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes recorded in
-``profiles/hbm_traffic_gate_up_t16.json`` (scaled by the counters' reading of a
-plain copy of known size), or null when that file is absent.
+better).  ``roofline`` is the dominant kernel, the layer's one expert launch as
+it runs in the layer: it routes the block in its prologue (from the step's
+router logits), streams the hit experts' gate/up rows, then the matching
+K-slices of their down rows (split-K down, partial y rows for the combine).
+HIP events on its launch stream bracket graph replays that hold only that
+kernel's launches (measurement mode of the library), one per step over the
+same rotation of weight sets and hidden blocks; achieved = its algorithmic
+bytes (int4 gate/up and down rows + bf16 scales of the hit experts and the
+shared expert, x in, partial y rows out) / mean launch duration.
+``traffic`` is the HBM bytes the same kernel moves per launch, from the
+rocprofv3 FETCH_SIZE / WRITE_SIZE passes recorded in
+``profiles/hbm_traffic_split_down_t16.json`` (scaled by the counters' reading
+of a plain copy of known size), or null when that file is absent.
+``stages`` also times the same layer with the down GEMM as a launch of its own.
 ``prefill`` reports the T=2048 layer in TFLOP/s against bf16 MFMA peak.
 ``cpu_baseline`` times the oracle's CPU restatement of the same layer.
 """
@@ -206,6 +209,23 @@ GATE_UP_BYTES_PER_EXPERT = 2 * 512 * 2048 // 2 + 2 * 512 * (2048 // 128) * 2   #
 DOWN_BYTES_PER_EXPERT = 2048 * 512 // 2 + 2048 * (512 // 128) * 2
 
 
+def split_part_rows(offsets, tokens, grid, strips=32, shared=True):
+    """Partial y rows the split-K down writes for one routing: pass P (16-row passes of every hit
+    expert in id order, then the shared expert's) is spread over workgroups
+    floor((G (x + 1) - 1) / U) of its first and last units x, each writing the pass's rows."""
+    counts = [int(c) for c in (offsets[1:] - offsets[:-1]).tolist()]
+    rows = [min(16, c - 16 * i) for c in counts if c > 0 for i in range((c + 15) // 16)]
+    if shared:
+        rows += [min(16, tokens - 16 * i) for i in range((tokens + 15) // 16)]
+    units = len(rows) * strips
+    total = 0
+    for p_, r in enumerate(rows):
+        b0 = (grid * (p_ * strips + 1) - 1) // units
+        b1 = (grid * (p_ + 1) * strips - 1) // units
+        total += r * (b1 - b0 + 1)
+    return total
+
+
 def time_stage(pkg, sets, blocks, top_k, steps, warmup, stage=None, given_logits=False):
     """Average launch duration of one expert-stage kernel, timed with HIP events.
 
@@ -215,17 +235,20 @@ def time_stage(pkg, sets, blocks, top_k, steps, warmup, stage=None, given_logits
     of those single-kernel steps is replayed between two events on torch's
     current stream (the stream the library launches on), so the timed region
     holds nothing but back-to-back launches of the kernel.  Returns the mean
-    duration per launch (ms) and the mean number of hit experts.
+    duration per launch (ms), the mean number of hit experts and the mean number of
+    partial y rows a split-K down launch writes for those routings.
     """
     stage = pkg.ops.STAGE_GATE_UP if stage is None else stage
     period = 24
     device = blocks[0].device
-    nbytes = pkg.ops.moe_workspace_bytes(blocks[0].shape[0], 2048, 512, 256, top_k, 128, True)
+    tokens = blocks[0].shape[0]
+    grid = torch.cuda.get_device_properties(device).multi_processor_count
+    nbytes = pkg.ops.moe_workspace_bytes(tokens, 2048, 512, 256, top_k, 128, True)
     wss = [torch.empty(nbytes, dtype=torch.uint8, device=device) for _ in range(period)]
     # with given_logits the calls pass each step's router logits, so the verify gate/up kernel
     # routes in its prologue exactly as inside the layer; else it reads the work table
     logits = [pkg.ops.router_logits(blocks[j % len(blocks)], sets[j % len(sets)][3]) for j in range(period)]
-    hits = []
+    hits, parts = [], []
 
     def call(j):
         gu, dn, sh, router = sets[j % len(sets)]
@@ -235,6 +258,7 @@ def time_stage(pkg, sets, blocks, top_k, steps, warmup, stage=None, given_logits
     for j in range(period):
         _, r, _ = call(j)
         hits.append(int((r.offsets[1:] > r.offsets[:-1]).sum().item()))
+        parts.append(split_part_rows(r.offsets.cpu(), tokens, grid))
     torch.cuda.synchronize()
 
     def step(j):
@@ -244,7 +268,7 @@ def time_stage(pkg, sets, blocks, top_k, steps, warmup, stage=None, given_logits
         ms = time_steps(step, steps, warmup, period)
     finally:
         pkg.ops.set_measure_stage(0)
-    return ms, statistics.mean(hits)
+    return ms, statistics.mean(hits), statistics.mean(parts)
 
 
 def time_stack(pkg, device, steps, warmup, context=4096, tokens=16):
@@ -346,8 +370,8 @@ def measured_mfma():
 
 
 def measured_traffic():
-    """HBM bytes per T=16 gate/up launch from the committed counter passes, or None."""
-    path = ROOT / "profiles" / "hbm_traffic_gate_up_t16.json"
+    """HBM bytes per T=16 split-K expert launch from the committed counter passes, or None."""
+    path = ROOT / "profiles" / "hbm_traffic_split_down_t16.json"
     if not path.is_file():
         return None
     rec = json.loads(path.read_text())
@@ -378,8 +402,10 @@ def _median_run(run, warmups=3, measured=10, budget_s=12.0):
     return statistics.median(times), len(times)
 
 
-def cpu_baseline(pkg, tokens, top_k):
-    """The oracle's CPU restatement of the same T=16 layer, shared expert included, on the host.
+def cpu_baseline(pkg, sets, blocks, top_k):
+    """The oracle's CPU restatement of the same T=16 layer, shared expert included, on the host,
+    on the GPU leg's own tensors: hidden block 0 and weight set 0, the hit experts' banks copied
+    to the host and taken back from the tiled to the portable order.
 
     Protocol: 3 warmups + 10 timed runs, median; torch intra-op threads = every CPU this
     process may run on.  ``value``: dense bf16 banks of the hit experts dequantised before the
@@ -392,39 +418,50 @@ def cpu_baseline(pkg, tokens, top_k):
 
     threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
     torch.set_num_threads(threads)
-    layer = pkg.synthetic.moe_layer(tokens, seed=0)
-    logits = oracle_moe.router_logits(layer.hidden, layer.router_weight)
+    gu_d, dn_d, sh_d, router = sets[0]
+    hidden = blocks[0].cpu()
+    tokens = hidden.shape[0]
+    logits = oracle_moe.router_logits(hidden, router.cpu())
     ids, _ = oracle_routing.topk(logits, top_k)
     hit = np.unique(ids).tolist()
-    gu, dn, sh = layer.gate_up, layer.down, layer.shared
 
-    def deq(bank, e=None):
-        return oracle_w4.dequantize_torch(bank.packed if e is None else bank.packed[e],
-                                          bank.scales if e is None else bank.scales[e], 128)
+    def portable(bank, e=None):
+        packed = bank.packed if e is None else bank.packed[e]
+        scales = bank.scales if e is None else bank.scales[e]
+        pk, sc = oracle_w4.from_tiled(packed.cpu().numpy(), scales.float().cpu().numpy())
+        return torch.from_numpy(pk), torch.from_numpy(sc)
+
+    host = {e: (portable(gu_d, e), portable(dn_d, e)) for e in hit}
+    sh_host = (portable(sh_d.gate_up), portable(sh_d.down), sh_d.gate_weight.cpu())
+
+    def deq(pair):
+        return oracle_w4.dequantize_torch(pair[0], pair[1], 128)
     # dense bf16 banks, materialised for the hit experts only (the others are never read)
-    gate_up = torch.zeros((gu.experts, gu.rows, gu.cols), dtype=torch.bfloat16)
-    down = torch.zeros((dn.experts, dn.rows, dn.cols), dtype=torch.bfloat16)
+    gate_up = torch.zeros((gu_d.experts, gu_d.rows, gu_d.cols), dtype=torch.bfloat16)
+    down = torch.zeros((dn_d.experts, dn_d.rows, dn_d.cols), dtype=torch.bfloat16)
     for e in hit:
-        gate_up[e], down[e] = deq(gu, e), deq(dn, e)
-    shared_dense = (deq(sh.gate_up), deq(sh.down), sh.gate_weight)
-    dense_s, n_dense = _median_run(lambda: oracle_moe.moe_dense(layer.hidden, logits, top_k, gate_up, down,
+        gate_up[e], down[e] = deq(host[e][0]), deq(host[e][1])
+    shared_dense = (deq(sh_host[0]), deq(sh_host[1]), sh_host[2])
+    layer_hidden = hidden
+    dense_s, n_dense = _median_run(lambda: oracle_moe.moe_dense(layer_hidden, logits, top_k, gate_up, down,
                                                                   shared=shared_dense))
     fly_s, n_fly = _median_run(lambda: oracle_moe.moe_dense(
-        layer.hidden, logits, top_k, None, None, dequantize=lambda e: (deq(gu, e), deq(dn, e)),
-        shared=(deq(sh.gate_up), deq(sh.down), sh.gate_weight)))
+        layer_hidden, logits, top_k, None, None, dequantize=lambda e: (deq(host[e][0]), deq(host[e][1])),
+        shared=(deq(sh_host[0]), deq(sh_host[1]), sh_host[2])))
     # config 1: the single W4A16 qlinear
     gen = torch.Generator().manual_seed(1)
     x1 = torch.randn((16, 2048), generator=gen).to(torch.bfloat16)
     w1 = pkg.synthetic.int4_weight(gen, (512, 2048), 128)
-    w1_dense = deq(w1)
+    w1_dense = deq((w1.packed, w1.scales))
     ql_s, _ = _median_run(lambda: torch.nn.functional.linear(x1, w1_dense), warmups=3, measured=10)
-    ql_fly_s, _ = _median_run(lambda: torch.nn.functional.linear(x1, deq(w1)), warmups=3, measured=10)
+    ql_fly_s, _ = _median_run(lambda: torch.nn.functional.linear(x1, deq((w1.packed, w1.scales))), warmups=3,
+                              measured=10)
     return {"value": round(dense_s * 1e6, 1), "unit": "us/layer", "cores": threads, "kind": "port",
             "cpu_model": _cpu_model(), "cpu_count": os.cpu_count(),
-            "sample": f"oracle.moe.moe_dense: the T={tokens} layer (router logits given, top-{top_k} over 256 "
-                      f"experts, {len(hit)} hit experts + the gated shared expert, fp32 combine) on dense bf16 "
-                      f"banks dequantised before timing; median of {n_dense} runs after 3 warmups, "
-                      f"torch threads={threads}",
+            "sample": f"oracle.moe.moe_dense: the GPU leg's T={tokens} layer (its hidden block 0 and weight set "
+                      f"0, router logits given, top-{top_k} over 256 experts, {len(hit)} hit experts + the gated "
+                      f"shared expert, fp32 combine) on dense bf16 banks dequantised before timing; median of "
+                      f"{n_dense} runs after 3 warmups, torch threads={threads}",
             "dequant_inclusive_us": round(fly_s * 1e6, 1), "dequant_inclusive_runs": n_fly,
             "qlinear_config1_us": round(ql_s * 1e6, 1), "qlinear_config1_dequant_inclusive_us": round(ql_fly_s * 1e6, 1)}
 
@@ -480,26 +517,30 @@ def main() -> int:
     all_bytes = (hits + 1) * (INT4_BYTES_PER_EXPERT + SCALE_BYTES_PER_EXPERT)
     layer_gbs = int4_bytes / (ms * 1e-3) / 1e9
     log("timing the expert kernels with HIP events")
-    # gate/up and down as separate launches (the default), and as one launch (opt-in)
-    lay_ms, lay_hits = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup, pkg.ops.STAGE_EXPERTS,
-                                  given_logits=True)
-    pkg.ops.set_fused_layer(True)
+    # the layer's expert kernel: the gate/up launch that routes the block and runs the split-K
+    # down (measurement of EXPERTS with the step's logits relaunches exactly that kernel)
+    split = pkg.ops.moe_split_down(tokens, 2048, 512, 256, top_k, 128, True)
+    lay_ms, lay_hits, lay_parts = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup,
+                                             pkg.ops.STAGE_EXPERTS, given_logits=True)
+    # the same layer with the down GEMM as a launch of its own, and its two expert kernels alone
+    pkg.ops.set_split_down(False)
     try:
-        fused_ms, _ = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup, pkg.ops.STAGE_EXPERTS,
-                                 given_logits=True)
-        fused_layer_ms = time_layer(pkg, sets, blocks, top_k, args.steps, args.warmup, ws)
+        two_layer_ms = time_layer(pkg, sets, blocks, top_k, args.steps, args.warmup, ws)
+        two_ms, _, _ = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup, pkg.ops.STAGE_EXPERTS,
+                                  given_logits=True)
+        gu_ms, gu_hits, _ = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup, given_logits=True)
+        stream_ms, _, _ = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup)
+        dn_ms, _, _ = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup, pkg.ops.STAGE_DOWN)
     finally:
-        pkg.ops.set_fused_layer(False)
-    gu_ms, gu_hits = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup, given_logits=True)
-    stream_ms, _ = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup)
-    dn_ms, _ = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup, pkg.ops.STAGE_DOWN)
-    # algorithmic bytes of one gate/up launch: the hit experts' and the shared expert's int4
-    # gate/up rows + bf16 scales, x (bf16) read, h (bf16) written; of both expert launches:
-    # gate/up and down rows + scales, x read, the fp32 y rows the combine reads written
+        pkg.ops.set_split_down(True)
+    # algorithmic bytes of the split launch: the hit experts' and the shared expert's int4 gate/up
+    # and down rows + bf16 scales, x (bf16) read, the fp32 partial y rows written (h stays in LDS);
+    # of the two-launch form's gate/up launch: gate/up rows + scales, x read, h (bf16) written
     rows = tokens * top_k + tokens
+    lay_bytes = ((lay_hits + 1) * (GATE_UP_BYTES_PER_EXPERT + DOWN_BYTES_PER_EXPERT) + tokens * 2048 * 2
+                 + lay_parts * 2048 * 4)
     gu_bytes = (gu_hits + 1) * GATE_UP_BYTES_PER_EXPERT + tokens * 2048 * 2 + rows * 512 * 2
-    lay_bytes = (lay_hits + 1) * (GATE_UP_BYTES_PER_EXPERT + DOWN_BYTES_PER_EXPERT) + tokens * 2048 * 2 + rows * 2048 * 4
-    achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
+    achieved = lay_bytes / (lay_ms * 1e-3) / 1e9
 
     result = {
         "metric": METRIC, "value": round(ms * 1e3, 2), "unit": "us/layer", "n_gpus": 1,
@@ -516,15 +557,18 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": "w4_verify_kernel<1, 16, unsigned short> (routing prologue + grouped gate/up "
-                               "+ SiLU*up, T=16, tiled banks)",
-                     "kernel_us": round(gu_ms * 1e3, 2), "hit_experts_mean": round(gu_hits, 2),
-                     "bytes_per_launch": int(gu_bytes)},
-        "stages": {"expert_stage_us": round(exp_ms * 1e3, 2), "down_kernel_us": round(dn_ms * 1e3, 2),
+                               "+ SiLU*up + split-K down, T=16, tiled banks)" if split else
+                               "w4_verify_kernel<1, 16, unsigned short> (routing prologue + grouped gate/up)",
+                     "kernel_us": round(lay_ms * 1e3, 2), "hit_experts_mean": round(lay_hits, 2),
+                     "partial_rows_mean": round(lay_parts, 1), "bytes_per_launch": int(lay_bytes)},
+        "stages": {"expert_stage_us": round(exp_ms * 1e3, 2),
+                   "split_down": bool(split),
+                   "two_launch_layer_us": round(two_layer_ms * 1e3, 2),
+                   "two_launch_expert_kernels_us": round(two_ms * 1e3, 2),
+                   "two_launch_gate_up_us": round(gu_ms * 1e3, 2),
+                   "two_launch_gate_up_gbs": round(gu_bytes / (gu_ms * 1e-3) / 1e9, 1),
+                   "two_launch_down_us": round(dn_ms * 1e3, 2),
                    "gate_up_stream_only_us": round(stream_ms * 1e3, 2),
-                   "expert_kernels_us": round(lay_ms * 1e3, 2),
-                   "expert_kernels_gbs": round(lay_bytes / (lay_ms * 1e-3) / 1e9, 1),
-                   "one_launch_expert_kernel_us": round(fused_ms * 1e3, 2),
-                   "one_launch_layer_us": round(fused_layer_ms * 1e3, 2),
                    "expert_int4_bytes": int(int4_bytes), "expert_weight_bytes": int(all_bytes),
                    "expert_stage_int4_gbs": round(int4_bytes / (exp_ms * 1e-3) / 1e9, 1)},
     }
@@ -534,8 +578,9 @@ def main() -> int:
         steps_p = max(5, args.steps // 10)
         ms_p = time_layer(pkg, sets, blocks_p, top_k, steps_p, max(2, args.warmup // 10), ws)
         tflops = moe_flops(2048, top_k) / (ms_p * 1e-3) / 1e12
-        gu_p_ms, _ = time_stage(pkg, sets, blocks_p, top_k, steps_p, max(2, args.warmup // 10))
-        dn_p_ms, _ = time_stage(pkg, sets, blocks_p, top_k, steps_p, max(2, args.warmup // 10), pkg.ops.STAGE_DOWN)
+        gu_p_ms, _, _ = time_stage(pkg, sets, blocks_p, top_k, steps_p, max(2, args.warmup // 10))
+        dn_p_ms, _, _ = time_stage(pkg, sets, blocks_p, top_k, steps_p, max(2, args.warmup // 10),
+                                   pkg.ops.STAGE_DOWN)
         gu_flops = 2 * (2048 * top_k + 2048) * 1024 * 2048
         gu_tf = gu_flops / (gu_p_ms * 1e-3) / 1e12
         result["prefill"] = {
@@ -559,7 +604,7 @@ def main() -> int:
         result["qlinear"] = time_qlinear(pkg, device, max(24, args.steps // 2), args.warmup)
     if not args.no_cpu_baseline:
         log("timing the CPU baseline")
-        result["cpu_baseline"] = cpu_baseline(pkg, tokens, top_k)
+        result["cpu_baseline"] = cpu_baseline(pkg, sets, blocks, top_k)
     print(json.dumps(result))
     return 0
 

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DFLASH_ABI_VERSION 5
+#define DFLASH_ABI_VERSION 6
 
 enum dflash_status {
   DFLASH_OK = 0,
@@ -177,6 +177,9 @@ int dflash_moe_experts_w4a16(const void* hidden, int64_t tokens, int64_t hidden_
  * caller's arrays exactly as dflash_moe_route defines them.  Mirrors
  * OriginalQuantizedWeights.moe (fused/quantization.py:181-202) and the
  * FusedOps.moe contract (fused/ops.py:108-123) over packed banks.
+ * For blocks of up to 32 tokens dflash_moe_workspace_bytes includes partial down
+ * rows sized for the current device's CU count (a split-K down GEMM that runs
+ * inside the gate/up launch): query it with the call's device current.
  */
 int dflash_moe_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, const float* router_logits,
                      const void* router_weight, int64_t top_k, const dflash_w4* gate_up, const dflash_w4* down,
@@ -186,21 +189,19 @@ int dflash_moe_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, co
                      void* stream);
 
 /*
- * One-launch expert FFN (no counterpart in the reference).  When enabled (process-wide,
- * off by default), a verify block (T <= 32) that dflash_moe_w4a16 routes inside its gate/up
- * launch, with one scale dtype for both banks, on a device of 8 XCDs, runs gate/up and down
- * as one launch: pass P belongs to XCD P % 8, whose workgroups (as the hardware placed
- * them) claim its gate/up, then its down ranges and hand h rows to each other in that XCD's
- * L2.  Same results as the two launches up to the order of fp32 sums inside a tile.
- * dflash_moe_fused_status_offset returns the byte offset in the workspace of that launch's
- * status word, cleared by every call: after the call it holds bit 0 when a workgroup read
- * an XCD id above 7 and bit 1 when a wait for gate/up rows gave up (the output is then
- * wrong); -1 when a layer of this shape runs the separate launches.  It needs the current
- * device (its CU and XCD counts).
+ * Split-K down GEMM of verify blocks (no counterpart in the reference, whose vendor path
+ * runs two grouped GEMMs, fused/quantization.py:193-199).  A block of up to 32 tokens that
+ * dflash_moe_w4a16 routes inside its gate/up launch, with banks of one scale dtype and H in
+ * {512, 1024, 2048}, runs the down GEMM in that launch too: each workgroup multiplies
+ * the h columns it produced by the matching K-slice of the down bank and writes fp32 partial
+ * rows, which the combine adds in a fixed order (deterministic; the fp32 summation order
+ * differs from the two-launch form).  dflash_set_split_down(0) turns it off process-wide
+ * (for comparisons; on by default); dflash_moe_split_down returns 1 when a call of this
+ * shape runs it on the current device, else 0.
  */
-int dflash_set_fused_layer(int enable);
-int64_t dflash_moe_fused_status_offset(int64_t tokens, int64_t hidden_size, int64_t inter_size, int64_t experts,
-                                       int64_t top_k, int64_t group_size, int has_shared);
+int dflash_set_split_down(int enable);
+int dflash_moe_split_down(int64_t tokens, int64_t hidden_size, int64_t inter_size, int64_t experts, int64_t top_k,
+                          int64_t group_size, int has_shared, int32_t scale_dtype, int32_t layout);
 
 /*
  * dflash_moe_w4a16 without a workspace: the same layer, arguments and results, with its
@@ -230,12 +231,11 @@ int dflash_moe_w4a16_noalloc(const void* hidden, int64_t tokens, int64_t hidden_
  * output again (out is not written).  On the verify path (T <= 32) the gate/up
  * kernel also routes the block in its prologue; in measurement mode it does so
  * only when the call passes router_logits (else it reads the work table).
- * Where dflash_moe_w4a16 runs gate/up and down as one launch (T <= 32, the block
- * routed in that launch), DFLASH_STAGE_EXPERTS with router_logits relaunches
- * that kernel; GATE_UP and DOWN alone, or EXPERTS without router_logits, run
- * the two separate verify kernels of the same layer instead (their intermediate
- * rows can differ from the one launch's in the last bit: the two split a tile's
- * k-blocks over waves differently).
+ * Where dflash_moe_w4a16 runs the down GEMM inside the gate/up launch (a verify
+ * block routed in that launch, dflash_moe_split_down), DFLASH_STAGE_EXPERTS with
+ * router_logits relaunches that one kernel; GATE_UP and DOWN alone, or EXPERTS
+ * without router_logits, run the separate verify gate/up and down kernels of
+ * the same layer instead.
  * DFLASH_STAGE_NONE restores full calls.  Process-wide.
  */
 enum dflash_stage {

@@ -12,7 +12,7 @@ from pathlib import Path
 PACKAGE_DIR = Path(__file__).resolve().parent
 LIBRARY_PATH = PACKAGE_DIR / "libdflash_hip.so"
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 DTYPE_BF16 = 0
 DTYPE_F32 = 1
 DTYPE_F16 = 2
@@ -68,8 +68,9 @@ SIGNATURES = {
                                         _P, _P, _P, _P, _SZ, _P]),
     "dflash_moe_w4a16_noalloc": (ctypes.c_int, [_P, _I64, _I64, _P, _P, _I64, _W4P, _W4P, _W4P, _W4P, _P, _P, _P, _P,
                                                 _P, _P, _P, _P, _P]),
-    "dflash_set_fused_layer": (ctypes.c_int, [ctypes.c_int]),
-    "dflash_moe_fused_status_offset": (_I64, [_I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_int]),
+    "dflash_set_split_down": (ctypes.c_int, [ctypes.c_int]),
+    "dflash_moe_split_down": (ctypes.c_int, [_I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_int, ctypes.c_int32,
+                                             ctypes.c_int32]),
     "dflash_set_measure_stage": (ctypes.c_int, [ctypes.c_int]),
 }
 

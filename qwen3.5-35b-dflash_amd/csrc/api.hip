@@ -98,17 +98,24 @@ RouteLayout route_layout(int64_t T, int64_t k, int64_t E) {
 // The down plan of the verify path covers persistent grids up to this many workgroups.
 constexpr int kDownPlanMaxGrid = 1024;
 
+// Split-K down of the verify path: rows per partial segment (min(16, T)) and the partial
+// y rows it may write on a grid of `grid` workgroups: rps * (grid + passes), at most
+// min(E, T k) * ceil(T / 16) routed passes plus ceil(T / 16) of the shared expert.
+int64_t part_rps(int64_t T) { return std::min<int64_t>(16, T); }
+int64_t verify_pass_cap(int64_t T, int64_t E, int64_t k, bool shared) {
+  const int64_t tp = (T + 15) / 16;
+  return std::min(E, T * k) * tp + (shared ? tp : 0);
+}
+
 struct MoeLayout {
   RouteLayout route;
-  size_t logits, x_il, xneg, gate, h, hpart, y, down_plan, total;
-  // fused layer launch: per XCD a block of ready_stride words (its per-pass counts, then its
-  // two queues), then the done count and the error word on lines of their own; ready_words
-  // covers them all (the front launch clears them)
-  size_t ready, done, err, ready_words;
-  int ready_stride;
+  size_t logits, x_il, xneg, gate, h, hpart, y, down_plan;
+  size_t ypart, row_seg;  // split-K down (parts_grid > 0): partial y rows, per slot row its partials
+  int parts_grid;         // the grid the partial rows cover, 0 without them
+  size_t total;
 };
 
-MoeLayout moe_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, bool shared) {
+MoeLayout moe_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, bool shared, int parts_grid = 0) {
   MoeLayout L;
   L.route = route_layout(T, k, E);
   Carver c;
@@ -122,14 +129,13 @@ MoeLayout moe_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, bool
   L.hpart = c.take(4 * rows * (I / 16));
   L.y = c.take(4 * rows * H);
   L.down_plan = c.take(48 * static_cast<size_t>(kDownPlanMaxGrid));
-  // a pass holds at least one row: at most T*k + T passes, ceil of an eighth per XCD; each
-  // XCD's block (counts + 2 queues) rounded up to 128-byte lines
-  const int64_t local = (T * k + T + dflash::kXcds - 1) / dflash::kXcds;
-  L.ready_stride = static_cast<int>(std::min<int64_t>((local + 2 + 31) / 32 * 32, int64_t(1) << 28));
-  L.ready_words = static_cast<size_t>(dflash::kXcds) * L.ready_stride + 64;
-  L.ready = c.take(4 * L.ready_words);
-  L.done = L.ready + 4 * static_cast<size_t>(dflash::kXcds) * L.ready_stride;
-  L.err = L.done + 128;
+  L.parts_grid = parts_grid;
+  L.ypart = L.row_seg = 0;
+  if (parts_grid > 0) {
+    const int64_t prow = part_rps(T) * (parts_grid + verify_pass_cap(T, E, k, shared));
+    L.ypart = c.take(4 * static_cast<size_t>(prow) * H);
+    L.row_seg = c.take(8 * rows);
+  }
   L.total = c.off;
   return L;
 }
@@ -177,18 +183,6 @@ int cu_count() {
   int n = cache[dev].load(std::memory_order_relaxed);
   if (n > 0) return n;
   if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-  cache[dev].store(n, std::memory_order_relaxed);
-  return n;
-}
-
-// XCDs (XCCs) of the current device, 0 when unknown.
-int xcc_count() {
-  static std::atomic<int> cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  int n = cache[dev].load(std::memory_order_relaxed);
-  if (n > 0) return n;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || n <= 0) return 0;
   cache[dev].store(n, std::memory_order_relaxed);
   return n;
 }
@@ -336,21 +330,6 @@ bool verify_fits(const MoeShapes& S, bool route, dflash::VerifyParams* gu, dflas
          verify_layout(kModeDown, T, I, H, E, k, sh, 0, dn);
 }
 
-// Fused layer launch (gate/up and down in one kernel, w4_layer_kernel): a verify block
-// that routes in the gate/up prologue, one scale dtype for both banks, a grid of whole
-// XCDs.  Fills the LDS layouts of both phases.
-std::atomic<int> g_fused_layer{0};  // dflash_set_fused_layer (process-wide)
-
-bool layer_fits(const MoeShapes& S, const dflash::VerifyParams& vgu, dflash::VerifyParams* lgu,
-                dflash::VerifyParams* ldn) {
-  using namespace dflash;
-  if (!g_fused_layer.load(std::memory_order_acquire)) return false;
-  if (!vgu.route || S.gu_f32 != S.dn_f32) return false;
-  if (cu_count() % kXcds != 0 || xcc_count() != kXcds) return false;
-  return layer_layout(static_cast<int>(S.T), static_cast<int>(S.H), static_cast<int>(S.I), static_cast<int>(S.E),
-                      static_cast<int>(S.k), S.shared ? 1 : 0, lgu, ldn);
-}
-
 // Routing outputs the gate/up launch writes when it routes in its prologue.
 struct RouteOut {
   bool logits_given;  // the caller's logits (valid in measurement mode too)
@@ -362,10 +341,25 @@ struct RouteOut {
   int32_t* offsets;
 };
 
-// `layer`: the fused launch's two phase layouts (layer_fits), or null.  A call that fits the
-// fused launch runs it, except in measurement of one stage (GATE_UP or DOWN alone) or without
-// the caller's logits in measurement mode, which run the two verify launches instead.
-int run_verify(const MoeShapes& S, dflash::VerifyParams gu, dflash::VerifyParams dn, const dflash::VerifyParams* layer,
+// Split-K down (fused_down in the gate/up launch): a verify block routed in the gate/up
+// prologue (one 32-lane row per token), banks of one scale type, H in {512, 1024, 2048}, a
+// workspace with the partial rows for this grid, and unit ranges of at most two passes.
+// Appends the LDS of the down phase to gu's layout.
+std::atomic<int> g_split_down{1};  // dflash_set_split_down (process-wide)
+
+bool fused_down_fits(const MoeShapes& S, dflash::VerifyParams* gu, const MoeLayout& L, int grid) {
+  using namespace dflash;
+  if (!g_split_down.load(std::memory_order_acquire)) return false;
+  if (gu->route != 2 || S.gu_f32 != S.dn_f32 || L.parts_grid < grid) return false;
+  if (S.H != 512 && S.H != 1024 && S.H != 2048) return false;
+  const int64_t strips = S.I / 16, cap = verify_pass_cap(S.T, S.E, S.k, S.shared);
+  if ((cap * strips + grid - 1) / grid > strips + 1) return false;  // a range of <= strips + 1 units spans <= 2 passes
+  return fused_down_layout(gu, static_cast<int>(S.I));
+}
+
+// fuse_down: run the down GEMM inside the gate/up launch (fused_down_fits was true); not in
+// measurement of GATE_UP or DOWN alone, which times the two verify launches instead.
+int run_verify(const MoeShapes& S, dflash::VerifyParams gu, dflash::VerifyParams dn, bool fuse_down,
                const RouteOut& ro, const int32_t* inv, const float* wts, void* ws, const MoeLayout& L,
                const dflash_w4* gate_up, const dflash_w4* down, const dflash_w4* sgu, const dflash_w4* sdn, void* out,
                hipStream_t stream) {
@@ -415,78 +409,70 @@ int run_verify(const MoeShapes& S, dflash::VerifyParams gu, dflash::VerifyParams
     gu.tok_out = at<int32_t>(ws, L.route.tok);
   }
   const int stage = g_measure.load(std::memory_order_acquire);
-  const bool fused = layer && gu.route && (stage == DFLASH_STAGE_NONE || stage == DFLASH_STAGE_EXPERTS);
+  const bool fused = fuse_down && gu.route && (stage == DFLASH_STAGE_NONE || stage == DFLASH_STAGE_EXPERTS);
   // the routing gate/up launch also plans the down launch's prologue (same workspace, next
-  // launch); a layer that fits the fused launch writes no plan, in measurement mode neither
+  // launch) when there is one
   const int grid = cu_count();
-  if (gu.route && !layer && grid <= kDownPlanMaxGrid) {
+  if (gu.route && !fused && grid <= kDownPlanMaxGrid) {
     gu.down_plan = at<int4>(ws, L.down_plan);
     gu.down_grid = grid;
     gu.down_strips = H / 32;
   }
-  if (!fused && stage_on(DFLASH_STAGE_GATE_UP)) launch_w4_verify(kModeGateUp, S.gu_f32, grid, gu, stream);
+  if (fused) {
+    gu.fuse_down = 1;
+    gu.dw = static_cast<const uint8_t*>(down->packed);
+    gu.ds = down->scales;
+    gu.dw_shared = S.shared ? static_cast<const uint8_t*>(sdn->packed) : nullptr;
+    gu.ds_shared = S.shared ? sdn->scales : nullptr;
+    gu.dw_stride = S.H * S.I / 2;
+    gu.ds_stride = S.H * (S.I / S.Gd);
+    gu.dH = H;
+    gu.dI = I;
+    gu.dG = static_cast<int>(S.Gd);
+    gu.ypart = at<float>(ws, L.ypart);
+    gu.row_seg = at<int2>(ws, L.row_seg);
+    gu.part_rps = static_cast<int>(part_rps(S.T));
+  } else {
+    gu.fuse_down = 0;
+  }
+  if (stage_on(DFLASH_STAGE_GATE_UP)) launch_w4_verify(kModeGateUp, S.gu_f32, grid, gu, stream);
   if (int r = launch_status("gate_up")) return r;
 
-  // down: N = H rows over K = I, routing-weight epilogue into y, then the combine
-  p.w = static_cast<const uint8_t*>(down->packed);
-  p.s = down->scales;
-  p.w_shared = S.shared ? static_cast<const uint8_t*>(sdn->packed) : nullptr;
-  p.s_shared = S.shared ? sdn->scales : nullptr;
-  p.w_stride = S.H * S.I / 2;
-  p.s_stride = S.H * (S.I / S.Gd);
-  p.G = static_cast<int>(S.Gd);
-  p.N = H;
-  p.K = I;
-  p.act = at<uint16_t>(ws, L.h);
-  p.act_neg = at<float>(ws, L.hpart);
-  p.neg_parts = 8;
-  p.out_bf16 = nullptr;
-  p.out_part = nullptr;
-  p.out_f32 = at<float>(ws, L.y);
-  p.slot_w = at<float>(ws, L.route.slot_w);
-  p.shared_gate = at<float>(ws, L.gate);
-  p.strips = H / 32;
-  dn.g = p;
-  dn.E = static_cast<int>(S.E);
-  // a plan exists only when this call's gate/up launch wrote one (measurement mode timing the
-  // down launch alone keeps the work table's pass count)
-  dn.down_plan = gu.down_plan && stage_on(DFLASH_STAGE_GATE_UP) ? gu.down_plan : nullptr;
-  if (fused) {
-    // both phases in one launch: the layer layouts, this call's parameters and routing outputs
-    VerifyParams lgu = layer[0], ldn = layer[1];
-    const int route_mode = lgu.route;
-    lgu.g = gu.g;
-    lgu.E = gu.E;
-    lgu.logits = gu.logits;
-    lgu.ids = gu.ids;
-    lgu.wts = gu.wts;
-    lgu.perm = gu.perm;
-    lgu.inv = gu.inv;
-    lgu.offsets = gu.offsets;
-    lgu.meta_out = gu.meta_out;
-    lgu.pass_table_out = gu.pass_table_out;
-    lgu.slot_w_out = gu.slot_w_out;
-    lgu.tok_out = gu.tok_out;
-    lgu.route = route_mode;
-    ldn.g = dn.g;
-    ldn.E = dn.E;
-    for (VerifyParams* v : {&lgu, &ldn}) {
-      v->down_plan = nullptr;
-      v->ready = at<int32_t>(ws, L.ready);
-      v->done = at<int32_t>(ws, L.done);
-      v->ready_stride = L.ready_stride;
-      v->chunks = grid / kXcds;
-      v->err = at<int32_t>(ws, L.err);
-      v->ready_target = I / 16;  // gate/up units (16-column pairs) per pass
-    }
-    launch_w4_layer(S.gu_f32, grid, lgu, ldn, stream);
-    if (int r = launch_status("layer")) return r;
-  } else {
+  if (!fused) {
+    // down: N = H rows over K = I, unweighted fp32 y (the combine applies the routing weights)
+    p.w = static_cast<const uint8_t*>(down->packed);
+    p.s = down->scales;
+    p.w_shared = S.shared ? static_cast<const uint8_t*>(sdn->packed) : nullptr;
+    p.s_shared = S.shared ? sdn->scales : nullptr;
+    p.w_stride = S.H * S.I / 2;
+    p.s_stride = S.H * (S.I / S.Gd);
+    p.G = static_cast<int>(S.Gd);
+    p.N = H;
+    p.K = I;
+    p.act = at<uint16_t>(ws, L.h);
+    p.act_neg = at<float>(ws, L.hpart);
+    p.neg_parts = 8;
+    p.out_bf16 = nullptr;
+    p.out_part = nullptr;
+    p.out_f32 = at<float>(ws, L.y);
+    p.slot_w = at<float>(ws, L.route.slot_w);
+    p.shared_gate = at<float>(ws, L.gate);
+    p.strips = H / 32;
+    dn.g = p;
+    dn.E = static_cast<int>(S.E);
+    // a plan exists only when this call's gate/up launch wrote one (measurement mode timing the
+    // down launch alone keeps the work table's pass count)
+    dn.down_plan = gu.down_plan && stage_on(DFLASH_STAGE_GATE_UP) ? gu.down_plan : nullptr;
     if (stage_on(DFLASH_STAGE_DOWN)) launch_w4_verify(kModeDown, S.dn_f32, grid, dn, stream);
     if (int r = launch_status("down")) return r;
   }
 
   if (measuring()) return DFLASH_OK;
+  if (fused) {
+    launch_combine_parts(at<float>(ws, L.ypart), at<int2>(ws, L.row_seg), gu.part_rps, inv, T, p.top_k, H,
+                         p.has_shared, wts, at<float>(ws, L.gate), static_cast<uint16_t*>(out), stream);
+    return launch_status("combine");
+  }
   // the verify down launch leaves y unweighted: the combine applies the routing weights
   launch_combine(at<float>(ws, L.y), inv, T, p.top_k, H, p.has_shared, wts, at<float>(ws, L.gate),
                  static_cast<uint16_t*>(out), stream);
@@ -835,7 +821,8 @@ int dflash_moe_route(const float* logits, int64_t tokens, int64_t experts, int64
 size_t dflash_moe_workspace_bytes(int64_t tokens, int64_t hidden_size, int64_t inter_size, int64_t experts,
                                   int64_t top_k, int64_t group_size, int has_shared) {
   if (tokens < 0 || hidden_size <= 0 || inter_size <= 0 || experts <= 0 || top_k <= 0 || group_size <= 0) return 0;
-  return moe_layout(tokens, hidden_size, inter_size, experts, top_k, has_shared != 0).total;
+  return moe_layout(tokens, hidden_size, inter_size, experts, top_k, has_shared != 0,
+                    tokens <= kVerifyMaxTokens ? cu_count() : 0).total;
 }
 
 int dflash_moe_experts_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, int64_t top_k,
@@ -885,9 +872,8 @@ int dflash_moe_experts_w4a16(const void* hidden, int64_t tokens, int64_t hidden_
     if (!measuring()) dflash::launch_table_prep(t, st);
     if (int r = launch_status("table_prep")) return r;
     if (verify)
-      return run_verify(S, vgu, vdn, nullptr, RouteOut{}, inv_perm, topk_weights, workspace, L, gate_up, down,
-                        shared_gate_up,
-                        shared_down, out, st);
+      return run_verify(S, vgu, vdn, false, RouteOut{}, inv_perm, topk_weights, workspace, L, gate_up, down,
+                        shared_gate_up, shared_down, out, st);
     return run_experts(S, inv_perm, workspace, L, gate_up, down, shared_gate_up, shared_down, out, st);
   } catch (...) {
     return fail(DFLASH_ERR_HIP, "unexpected host exception");
@@ -914,7 +900,9 @@ static int moe_w4a16_body(const void* hidden, int64_t tokens, int64_t hidden_siz
     if (!expert_offsets) return fail(DFLASH_ERR_INVALID_ARGUMENT, "expert_offsets is required");
     if (tokens > 0 && (!topk_ids || !topk_weights || !perm || !inv_perm))
       return fail(DFLASH_ERR_INVALID_ARGUMENT, "routing output arrays are required");
-    const MoeLayout L = moe_layout(S.T, S.H, S.I, S.E, S.k, S.shared);
+    // a caller workspace also holds the split-K down's partial rows (sized for this device's grid)
+    const MoeLayout L = moe_layout(S.T, S.H, S.I, S.E, S.k, S.shared,
+                                   !static_scratch && S.T <= kVerifyMaxTokens ? cu_count() : 0);
     if (static_scratch) {
       if (L.total > kScratchBytes)
         return fail(DFLASH_ERR_UNSUPPORTED, "moe_noalloc: this layer needs " + std::to_string(L.total) +
@@ -932,8 +920,7 @@ static int moe_w4a16_body(const void* hidden, int64_t tokens, int64_t hidden_siz
     dflash::VerifyParams vgu{}, vdn{};
     const bool verify = tokens > 0 && verify_fits(S, small, &vgu, &vdn);
     if (int r = check_tiled_moe(S, verify)) return r;
-    dflash::VerifyParams layer[2];
-    const bool fused = verify && layer_fits(S, vgu, &layer[0], &layer[1]);
+    const bool fused = verify && fused_down_fits(S, &vgu, L, cu_count());
     float* logits = router_logits ? const_cast<float*>(router_logits)
                                   : (logits_out ? logits_out : at<float>(workspace, L.logits));
     dflash::FrontParams f{};
@@ -957,10 +944,6 @@ static int moe_w4a16_body(const void* hidden, int64_t tokens, int64_t hidden_siz
       f.zero = at<uint32_t>(workspace, L.route.counts);
       f.zero_words = dflash::route_zero_words(T, E);
       f.n_zero = static_cast<int>(std::min<int64_t>(256, (f.zero_words + 2047) / 2048));
-    } else if (fused) {  // the fused launch's counters and error word start at zero
-      f.zero = at<uint32_t>(workspace, L.ready);
-      f.zero_words = static_cast<int64_t>(L.ready_words);
-      f.n_zero = 1;
     }
     if (!measuring()) dflash::launch_front(f, st);
     if (int r = launch_status("front")) return r;
@@ -983,7 +966,7 @@ static int moe_w4a16_body(const void* hidden, int64_t tokens, int64_t hidden_siz
     }
     if (tokens == 0) return DFLASH_OK;
     if (verify)
-      return run_verify(S, vgu, vdn, fused ? layer : nullptr,
+      return run_verify(S, vgu, vdn, fused,
                         RouteOut{router_logits != nullptr, logits, topk_ids, topk_weights, perm, inv_perm, expert_offsets},
                         inv_perm, topk_weights, workspace, L, gate_up, down, shared_gate_up, shared_down, out, st);
     return run_experts(S, inv_perm, workspace, L, gate_up, down, shared_gate_up, shared_down, out, st);
@@ -1014,27 +997,30 @@ int dflash_moe_w4a16_noalloc(const void* hidden, int64_t tokens, int64_t hidden_
                         perm, inv_perm, expert_offsets, nullptr, 0, true, stream);
 }
 
-int64_t dflash_moe_fused_status_offset(int64_t tokens, int64_t hidden_size, int64_t inter_size, int64_t experts,
-                                       int64_t top_k, int64_t group_size, int has_shared) {
-  try {
-    if (tokens <= 0 || check_route_args(tokens, experts, top_k) != DFLASH_OK) return -1;
-    if (hidden_size <= 0 || hidden_size % 512 || inter_size <= 0 || inter_size % 512) return -1;
-    const MoeShapes S{tokens, hidden_size, inter_size, experts, top_k, group_size, group_size, has_shared != 0,
-                      false, false, true, false};
-    const bool small = dflash::route_small_fits(static_cast<int>(tokens), static_cast<int>(experts),
-                                                static_cast<int>(top_k));
-    dflash::VerifyParams vgu{}, vdn{}, layer[2];
-    if (!verify_fits(S, small, &vgu, &vdn) || !layer_fits(S, vgu, &layer[0], &layer[1])) return -1;
-    return static_cast<int64_t>(moe_layout(S.T, S.H, S.I, S.E, S.k, S.shared).err);
-  } catch (...) {
-    return -1;
-  }
+int dflash_set_split_down(int enable) {
+  if (enable != 0 && enable != 1) return fail(DFLASH_ERR_INVALID_ARGUMENT, "enable must be 0 or 1");
+  g_split_down.store(enable, std::memory_order_release);
+  return DFLASH_OK;
 }
 
-int dflash_set_fused_layer(int enable) {
-  if (enable != 0 && enable != 1) return fail(DFLASH_ERR_INVALID_ARGUMENT, "enable must be 0 or 1");
-  g_fused_layer.store(enable, std::memory_order_release);
-  return DFLASH_OK;
+int dflash_moe_split_down(int64_t tokens, int64_t hidden_size, int64_t inter_size, int64_t experts, int64_t top_k,
+                          int64_t group_size, int has_shared, int32_t scale_dtype, int32_t layout) {
+  try {
+    if (tokens <= 0 || check_route_args(tokens, experts, top_k) != DFLASH_OK) return 0;
+    if (hidden_size <= 0 || hidden_size % 512 || inter_size <= 0 || inter_size % 512) return 0;
+    if (group_size != 128 && group_size != 256) return 0;
+    const bool f32 = scale_dtype == DFLASH_DTYPE_F32;
+    const MoeShapes S{tokens, hidden_size, inter_size, experts, top_k, group_size, group_size, has_shared != 0,
+                      f32, f32, true, layout == DFLASH_LAYOUT_TILED};
+    const bool small = dflash::route_small_fits(static_cast<int>(tokens), static_cast<int>(experts),
+                                                static_cast<int>(top_k));
+    dflash::VerifyParams vgu{}, vdn{};
+    if (!verify_fits(S, small, &vgu, &vdn)) return 0;
+    const MoeLayout L = moe_layout(S.T, S.H, S.I, S.E, S.k, S.shared, S.T <= kVerifyMaxTokens ? cu_count() : 0);
+    return fused_down_fits(S, &vgu, L, cu_count()) ? 1 : 0;
+  } catch (...) {
+    return 0;
+  }
 }
 
 #ifdef DFLASH_TIMELINE

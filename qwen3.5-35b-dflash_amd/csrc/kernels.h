@@ -207,18 +207,25 @@ struct VerifyParams {
   // launch (null: neither).  down_grid / down_strips: the down launch's grid and strips.
   int4* down_plan;
   int down_grid, down_strips;
-  // fused layer launch (w4_layer_kernel): pass P belongs to part x = P % 8 (part-local index
-  // j = P / 8), which the workgroups running on XCD x take, `chunks` contiguous unit ranges
-  // per phase, claimed from the part's queues.  Per part a block of ready_stride words:
-  // per-pass counts of finished gate/up units [j] (a down range waits for ready_target), then
-  // the gate/up and the down queue (its last two words).  done counts the workgroups past
-  // their last wait; the last one returns every word to zero (zero on entry, left zero).
-  // err[0] gets bit 0 when a workgroup reads an XCD id above 7, bit 1 when a wait gave up.
-  int fused;
-  int32_t* ready;
-  int32_t* done;
-  int32_t* err;
-  int ready_stride, ready_target, chunks;
+  // split-K down in the gate/up launch (gate/up with in-kernel routing only): each workgroup
+  // keeps the h columns of its unit range in LDS (lds_h: two pass slots x 16 rows x I, bf16
+  // octet-interleaved, zero outside the range; lds_hstart: -136 * sum of each 32-column
+  // quarter of each row) and multiplies them by the matching K-slice of the down bank (the
+  // gate/up bank's layout and scale type), writing one fp32 partial y row per pass row into
+  // ypart row 16 * (b + P) + r (workgroup b, pass P, pass row r; b + P never repeats).
+  // Workgroup 0 writes row_seg: per slot row its first partial row and partial count
+  // (consecutive partials 16 rows apart), which the combine sums in workgroup order.
+  int fuse_down;
+  const uint8_t* dw;         // down bank [E][H][I/2], shared expert's [H][I/2]
+  const void* ds;
+  const uint8_t* dw_shared;
+  const void* ds_shared;
+  int64_t dw_stride, ds_stride;  // bytes / scale elements per expert
+  int dH, dI, dG;
+  float* ypart;
+  int2* row_seg;
+  int part_rps;              // rows per partial segment: min(16, T)
+  int lds_h, lds_hstart;
 };
 #ifdef DFLASH_TIMELINE
 // Profiling build: phase timestamps of the verify and tile launches (timeline.py).
@@ -231,13 +238,15 @@ int timeline_tile_clear();
 // caller keeps the separate routing / streaming kernels then).
 bool verify_layout(int mode, int T, int K, int N, int E, int k, int has_shared, int route, VerifyParams* vp);
 void launch_w4_verify(int mode, bool fp32_scales, int grid, const VerifyParams& vp, hipStream_t stream);
-// Gate/up (routing in its prologue) and down in one launch: LDS layouts of both phases
-// (pass descriptors and slot tokens shared, the rest reused); false when they do not fit
-// or the block cannot route in the prologue.  For devices of 8 XCDs; the grid is the CU
-// count, chunks = grid / 8.
-constexpr int kXcds = 8;
-bool layer_layout(int T, int H, int I, int E, int k, int has_shared, VerifyParams* gu, VerifyParams* dn);
-void launch_w4_layer(bool fp32_scales, int grid, const VerifyParams& gu, const VerifyParams& dn, hipStream_t stream);
+// LDS the split-K down adds to a routing gate/up launch (two pass slots of h, quarter sums);
+// fused_down_layout appends it to a gate/up layout whose block routes in the prologue with
+// one 32-lane row per token, false when it does not fit.
+int fused_down_lds(int I);
+bool fused_down_layout(VerifyParams* vp, int I);
+// out = bf16(sum over slots of w * (sum of the slot row's partial y rows)) (+ gate * shared row),
+// partial rows as VerifyParams::row_seg lists them, fp32 in slot and partial order.
+void launch_combine_parts(const float* ypart, const int2* row_seg, int rps, const int32_t* inv, int T, int k, int H,
+                          int has_shared, const float* wts, const float* gate, uint16_t* out, hipStream_t stream);
 // LDS-tiled kernel for long prefill (w4_tile.hip): 96-row passes, column tiles of 512
 // (p.strips = I / 256 for gate_up, H / 512 for down), K % 512 == 0; its gate_up writes one
 // -136*sum(h) per 128 columns and its down reads them that way; its down writes weighted

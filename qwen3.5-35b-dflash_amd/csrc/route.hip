@@ -842,6 +842,51 @@ __global__ __launch_bounds__(64) void combine_kernel(const YT* __restrict__ y, c
   }
 }
 
+// Combine of the split-K down: a slot row's y is the sum of its partial rows (row_seg: first
+// partial row and count, consecutive partials part_rps rows apart, in workgroup order), then
+// weighted and added over the slots as combine_kernel does.  grid = (T, H / 512), block = 64.
+__global__ __launch_bounds__(64) void combine_parts_kernel(const float* __restrict__ y, const int2* __restrict__ seg,
+                                                           int rps, const int32_t* __restrict__ inv, int T, int k,
+                                                           int H, int has_shared, const float* __restrict__ wts,
+                                                           const float* __restrict__ gate, uint16_t* __restrict__ out) {
+  const int t = blockIdx.x;
+  const int c = (blockIdx.y * 64 + threadIdx.x) * 8;
+  const int nrows = k + (has_shared ? 1 : 0);
+  if (c >= H) return;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < nrows; ++s) {
+    const int row = s < k ? ld_const(inv, t * k + s) : T * k + t;
+    const int2 sg = seg[row];
+    const float w = s < k ? ld_const(wts, t * k + s) : ld_const(gate, t);
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int j0 = 0; j0 < sg.y; j0 += 4) {
+      float4 a[4], b[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {  // four partials in flight together
+        const int64_t r = static_cast<int64_t>(sg.x) + static_cast<int64_t>(rps) * min(j0 + j, sg.y - 1);
+        const float4* src = reinterpret_cast<const float4*>(y + r * H + c);
+        a[j] = src[0];
+        b[j] = src[1];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (j0 + j < sg.y) {
+          v[0] += a[j].x; v[1] += a[j].y; v[2] += a[j].z; v[3] += a[j].w;
+          v[4] += b[j].x; v[5] += b[j].y; v[6] += b[j].z; v[7] += b[j].w;
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] += v[i] * w;
+  }
+  uint4 o;
+  o.x = f32_to_bf16(acc[0]) | (static_cast<uint32_t>(f32_to_bf16(acc[1])) << 16);
+  o.y = f32_to_bf16(acc[2]) | (static_cast<uint32_t>(f32_to_bf16(acc[3])) << 16);
+  o.z = f32_to_bf16(acc[4]) | (static_cast<uint32_t>(f32_to_bf16(acc[5])) << 16);
+  o.w = f32_to_bf16(acc[6]) | (static_cast<uint32_t>(f32_to_bf16(acc[7])) << 16);
+  *reinterpret_cast<uint4*>(out + static_cast<int64_t>(t) * H + c) = o;
+}
+
 // ---------------------------------------------------------------------------
 // host launchers
 // 32 x 64 tiles read 384 KB each: they pay only with enough of them to fill the CUs (T=2048 at
@@ -908,6 +953,13 @@ void launch_combine_bf16(const uint16_t* y, const int32_t* inv, int T, int k, in
   if (T <= 0) return;
   hipLaunchKernelGGL(combine_kernel<uint16_t>, dim3(T, (H + 511) / 512), dim3(64), 0, stream, y, inv, T, k, H,
                      has_shared, nullptr, nullptr, out);
+}
+
+void launch_combine_parts(const float* ypart, const int2* row_seg, int rps, const int32_t* inv, int T, int k, int H,
+                          int has_shared, const float* wts, const float* gate, uint16_t* out, hipStream_t stream) {
+  if (T <= 0) return;
+  hipLaunchKernelGGL(combine_parts_kernel, dim3(T, (H + 511) / 512), dim3(64), 0, stream, ypart, row_seg, rps, inv, T,
+                     k, H, has_shared, wts, gate, out);
 }
 
 }  // namespace dflash

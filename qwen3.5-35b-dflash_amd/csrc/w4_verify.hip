@@ -69,24 +69,11 @@ constexpr int kVLds = 158 * 1024;  // one persistent workgroup per CU
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
-// Cache policy of a vector memory load: sc1 (device scope) makes it skip the CU's L1, so it
-// reads this XCD's L2, where other CUs of the XCD left their stores.  (sc0 alone, workgroup
-// scope, may still hit in L1.)
-constexpr int kCacheSc1 = 16;
-
-__device__ __forceinline__ void dma16(buf_rsrc r, void* dst, uint32_t voff, uint32_t soff, int cpol = 0) {
-  if (cpol == kCacheSc1)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)dst, 16, static_cast<int>(voff), static_cast<int>(soff), 0,
-                                             kCacheSc1);
-  else
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)dst, 16, static_cast<int>(voff), static_cast<int>(soff), 0, 0);
+__device__ __forceinline__ void dma16(buf_rsrc r, void* dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)dst, 16, static_cast<int>(voff), static_cast<int>(soff), 0, 0);
 }
-__device__ __forceinline__ void dma4(buf_rsrc r, void* dst, uint32_t voff, uint32_t soff, int cpol = 0) {
-  if (cpol == kCacheSc1)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)dst, 4, static_cast<int>(voff), static_cast<int>(soff), 0,
-                                             kCacheSc1);
-  else
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)dst, 4, static_cast<int>(voff), static_cast<int>(soff), 0, 0);
+__device__ __forceinline__ void dma4(buf_rsrc r, void* dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)dst, 4, static_cast<int>(voff), static_cast<int>(soff), 0, 0);
 }
 
 // XCD id of the executing workgroup (hardware register).
@@ -117,44 +104,20 @@ __device__ __forceinline__ void tl_mark(int mode, int slot, bool lane0_of_every_
 __device__ __forceinline__ void tl_mark(int, int, bool = false) {}
 #endif
 
-// Polls a workgroup may spend waiting over its whole down range (~0.1-0.4 s).
-constexpr int kSpinBudget = 200000;
-
-// Count word of part-local pass j of part x, and the part's gate/up (phase 0) and down
-// (phase 1) queues, its last two words: each part's words fill cache lines of their own.
-__device__ __forceinline__ int32_t* ready_word(const VerifyParams& vp, int part, int j) {
-  return vp.ready + part * vp.ready_stride + j;
-}
-__device__ __forceinline__ int32_t* queue_word(const VerifyParams& vp, int part, int phase) {
-  return vp.ready + part * vp.ready_stride + vp.ready_stride - 2 + phase;
-}
-
-// The unit range of a verify_gemm call: part `part` of `parts` (pass P is part P % parts's
-// local pass P / parts), its range `rank` of `ranks` contiguous ones.
-struct Split {
-  int part, parts, rank, ranks;
-};
-
-// Bounded wait (one thread) until each of the n count words of consecutive part-local passes
-// reads `target` finished gate/up units (device-scope atomics and loads: the load skips L1,
-// and the count is exact once it reads the target).  Every poll spends one of the workgroup's
-// budget (returned: what is left); once it is spent the wait sets err bit 1 and returns at
-// once, now and at every later call (the launch then ends with wrong down rows, never hangs).
-__device__ __noinline__ int wait_ready(int32_t* words, int n, int target, int32_t* err, int budget) {
-  for (int j = 0; j < n; ++j) {
-    while (__hip_atomic_load(words + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-      if (--budget < 0) {
-        __hip_atomic_fetch_or(err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return budget;
-      }
-      __builtin_amdgcn_s_sleep(1);
-    }
-  }
-  return budget;
-}
-
 // Opaque to the optimiser: the value must exist in registers at this point.
 __device__ __forceinline__ void pin(f32x4& v) { asm volatile("" : "+v"(v)); }
+
+// Split-K down: the partial y rows of row r of pass P.  Workgroup b of G takes units
+// [floor(U b / G), floor(U (b + 1) / G)) of the U = passes * strips unit list, so unit x lies
+// in workgroup floor((G (x + 1) - 1) / U); pass P's first and last units give its first and
+// last workgroups, and workgroup b writes the partial of (b, P) at row rps * (b + P) + r
+// (rps: rows per segment, min(16, T)).  Returns (first partial row, partial count).
+__device__ __forceinline__ int2 part_rows(const VerifyParams& vp, int P, int r, int total_passes) {
+  const int64_t S = vp.g.strips, G = gridDim.x, U = static_cast<int64_t>(total_passes) * S;
+  const int b0 = static_cast<int>((G * (P * S + 1) - 1) / U);
+  const int b1 = static_cast<int>((G * (P + 1) * S - 1) / U);
+  return make_int2(vp.part_rps * (b0 + P) + r, b1 - b0 + 1);
+}
 
 // ---------------------------------------------------------------------------
 // In-kernel routing of the block (512 threads, T <= 32, E <= 1024).  Leaves
@@ -408,7 +371,8 @@ __device__ int route_rows(const VerifyParams& vp, RowKeys<kPR> keys, char* lds, 
   float* rw = reinterpret_cast<float*>(cnt + 256);                // [T*k] routing weight of every flat pair
   int* rid = reinterpret_cast<int*>(rw + 512);                    // [T*k] expert of every flat pair
   int* wtot = rid + 512;                                          // [3][4] wave totals: slot rows, passes, hits
-  uint32_t* map_words = reinterpret_cast<uint32_t*>(wtot + 12);   // [E][tpad] bytes: slot + 1, or 0
+  int* pfirst = wtot + 12;                                        // [256] first pass of every expert
+  uint32_t* map_words = reinterpret_cast<uint32_t*>(pfirst + 256);  // [E][tpad] bytes: slot + 1, or 0
   uint8_t* map = reinterpret_cast<uint8_t*>(map_words);
   for (int i = tid; i < 256; i += kVThreads) cnt[i] = 0;
   for (int i = tid; i < (E * tpad) / 4; i += kVThreads) map_words[i] = 0u;
@@ -493,6 +457,7 @@ __device__ int route_rows(const VerifyParams& vp, RowKeys<kPR> keys, char* lds, 
   }
   const int off = ba + ia - c, p0 = bc + ic - np;
   if (tid < E) {
+    pfirst[tid] = p0;
     if (out) vp.offsets[tid] = off;
     for (int i = 0; i < np; ++i) {
       const int4 d = make_int4(tid, off, c, 16 * i);
@@ -511,6 +476,8 @@ __device__ int route_rows(const VerifyParams& vp, RowKeys<kPR> keys, char* lds, 
     vp.meta_out[0] = hits;
     vp.meta_out[1] = routed + shared_passes;
   }
+  const int total = routed + shared_passes;
+  if (out && vp.fuse_down && vp.g.has_shared && tid < T) vp.row_seg[T * k + tid] = part_rows(vp, routed + (tid >> 4), tid & 15, total);
   lds_barrier();  // every count is read: cnt becomes each expert's first slot row
   if (tid < E) cnt[tid] = off;
   lds_barrier();
@@ -531,6 +498,7 @@ __device__ int route_rows(const VerifyParams& vp, RowKeys<kPR> keys, char* lds, 
     const int pos = cnt[e] + before;
     tok[pos] = tt;
     if (out) {
+      if (vp.fuse_down) vp.row_seg[pos] = part_rows(vp, pfirst[e] + (before >> 4), before & 15, total);
       vp.perm[pos] = i;
       vp.inv[i] = pos;
       vp.slot_w_out[pos] = rw[i];
@@ -628,6 +596,10 @@ __device__ __forceinline__ int verify_passes(const VerifyParams& vp, char* lds) 
   int* lds_tok = reinterpret_cast<int*>(lds + vp.lds_tok);
   int4* lds_pdesc = reinterpret_cast<int4*>(lds + vp.lds_pdesc);
   if (kMode == kModeGateUp && vp.route == 2) {
+    if (vp.fuse_down) {  // h of the workgroup's unit range, zero outside it (the routing's barriers order this)
+      uint4* h = reinterpret_cast<uint4*>(lds + vp.lds_h);
+      for (int i = threadIdx.x; i < (2 * 16 * vp.dI * 2) / 16; i += kVThreads) h[i] = make_uint4(0u, 0u, 0u, 0u);
+    }
     if (vp.E <= 128) {
       const RowKeys<4> keys = route_rows_load<4>(vp);
       stage_x<kMode, kNKB>(vp, lds);
@@ -652,11 +624,10 @@ __device__ __forceinline__ int verify_passes(const VerifyParams& vp, char* lds) 
   return ld_const(vp.g.meta, 1);
 }
 
-// The streaming GEMM of one verify launch over `total_passes` passes: the units of range
-// sp.rank of part sp.part (linear mode: every workgroup's strided share).
+// The streaming GEMM of one verify launch over `total_passes` passes: workgroup b takes the
+// b-th of gridDim.x equal contiguous ranges of the unit list (linear mode: a strided share).
 template <int kMode, int kNKB, typename ScaleT>
-__device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, const int total_passes,
-                                            const Split sp) {
+__device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, const int total_passes) {
   const W4StreamParams& p = vp.g;
   constexpr int kK = kNKB * 128;
   constexpr int kRS = kK * 2 + 16;                  // LDS row stride (bytes) of an activation row
@@ -676,13 +647,8 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
   f32x4* lds_part = reinterpret_cast<f32x4*>(lds + vp.lds_part);  // [wave][2][64]
 
   const int strips = p.strips;
-  // fused layer launch: part x's passes (global index P = x + 8 j) and a claimed range of
-  // them; else one part, one range per workgroup.  Below, a pass index is part-local (j)
-  // unless named global.
-  const int parts = sp.parts, part = sp.part, rank = sp.rank, ranks = sp.ranks;
-  const int local_passes = total_passes > part ? (total_passes - part + parts - 1) / parts : 0;
-  auto gpass = [&](int j) { return part + parts * j; };
-  const int64_t total_units = static_cast<int64_t>(local_passes) * strips;
+  const int rank = static_cast<int>(blockIdx.x), ranks = static_cast<int>(gridDim.x);
+  const int64_t total_units = static_cast<int64_t>(total_passes) * strips;
   // linear mode: workgroup b runs units b, b + G, b + 2G, ... (G = grid), so at any moment the
   // workgroups stream one contiguous window of the weights (contiguous ranges per workgroup
   // leave ~2048 streams a fixed stride apart, which streamed up to 10% slower); its virtual
@@ -728,21 +694,18 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
     return make_int4(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
                      __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w));
   };
-  // descriptor of global pass P before the chunk is staged: a fused launch holds every pass
-  // in LDS since its routing prologue (the work table in memory is another XCD's to write)
+  // descriptor of pass P before the chunk is staged
   auto early_desc = [&](int P) -> int4 {
-    if (vp.fused) return lds_desc(P);
     return P == plan_p ? plan_d0 : P == plan_p + 1 ? plan_d1 : ld_const_int4(p.pass_table, P);
   };
   // pass descriptors: all of them after in-kernel routing, else the chunk's (staged below)
   int pd_base = 0;
   auto pass_desc = [&](int j) -> int4 {
     if (kMode == kModeLinear) return make_int4(0, 0, p.M, j * 16);
-    return lds_desc(vp.fused ? gpass(j) : j - pd_base);
+    return lds_desc(j - pd_base);
   };
 
   const bool chunked = kMode == kModeDown || (kMode == kModeGateUp && vp.gather);
-  int spin_budget = kSpinBudget;  // fused down: polls left to this workgroup's waits (thread 0)
   const int chunk_passes = chunked ? vp.chunk_passes : max(P_last - P_first + 1, 1);
   for (int Pc = P_first; Pc <= P_last; Pc += chunk_passes) {
     const int Pc_end = min(P_last + 1, Pc + chunk_passes);
@@ -781,6 +744,10 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
           const uint16_t hb = f32_to_bf16(silu(t0[e]) * t1[e]);
           const int hrow = shared ? p.T * p.top_k + m : cd.y + m;
           if (valid) p.out_bf16[static_cast<int64_t>(hrow) * inter + octet_slot(row0 + lr)] = hb;
+          if (valid && vp.fuse_down) {  // pass slot P - P_first of the split-K down (its range spans at most two)
+            uint16_t* lh = reinterpret_cast<uint16_t*>(lds + vp.lds_h);
+            lh[((P - P_first) * 16 + 4 * kq + e) * inter + octet_slot(row0 + lr)] = hb;
+          }
           const float part = row16_sum(valid ? bf16_to_f32(hb) : 0.f);
           if (valid && lr == 0) p.out_part[static_cast<int64_t>(hrow) * (inter >> 4) + strip] = -kDequantOffset * part;
         } else {
@@ -807,7 +774,7 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
         // before the staging barrier the descriptor comes from the work table (s_load),
         // except after in-kernel routing, whose table is only in LDS
         const int4 d = staged || (kMode == kModeGateUp && vp.route) || kMode == kModeLinear
-                           ? pass_desc(P) : early_desc(gpass(P));
+                           ? pass_desc(P) : early_desc(P);
         const bool shared = kMode != kModeLinear && d.x < 0;
         const int64_t e = kMode == kModeLinear ? 0 : d.x;
         const uint8_t* wbase = shared ? p.w_shared : p.w + e * p.w_stride;
@@ -887,40 +854,30 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
         // loads so the prologue's weight loads are not waited for ahead of them
         pd_base = Pc;
         const int npass = Pc_end - Pc;
-        if (!vp.fused) {
-          const buf_rsrc tr = make_rsrc(p.pass_table, static_cast<uint32_t>(total_passes) * 16);
-          if (wave == 0)
-            dma16(tr, lds_pdesc, static_cast<uint32_t>(min(Pc + lane, total_passes - 1) * 16), 0);
-        } else {
-          // fused launch: the chunk's h rows are written by this XCD's workgroups during this
-          // launch; wait until every gate/up unit of each of its passes has been counted
-          if (tid == 0)
-            spin_budget = wait_ready(ready_word(vp, part, Pc), Pc_end - Pc, vp.ready_target, vp.err, spin_budget);
-          __syncthreads();
-        }
-        // a fused launch reads h through the XCD's L2 (its writers are other CUs of this XCD)
-        const int cpol = vp.fused ? kCacheSc1 : 0;
+        const buf_rsrc tr = make_rsrc(p.pass_table, static_cast<uint32_t>(total_passes) * 16);
+        if (wave == 0)
+          dma16(tr, lds_pdesc, static_cast<uint32_t>(min(Pc + lane, total_passes - 1) * 16), 0);
         const int hrows = p.T * p.top_k + (p.has_shared ? p.T : 0);
         const buf_rsrc hr = make_rsrc(p.act, static_cast<uint32_t>(hrows) * kK * 2);
         constexpr int kBlk = kK / 512;
         for (int i = wave; i < npass * 16 * kBlk; i += kVWaves) {
           const int rr = i / kBlk, bl = i - rr * kBlk;
-          const int4 d = early_desc(gpass(Pc + rr / 16));
+          const int4 d = early_desc(Pc + rr / 16);
           const int base = d.x < 0 ? p.T * p.top_k : d.y;
           const int row = base + min(d.w + (rr & 15), d.z - 1);
           dma16(hr, lds_a + rr * kRS + bl * 1024, static_cast<uint32_t>(lane * 16),
-                static_cast<uint32_t>((row * kK + bl * 512) * 2), cpol);
+                static_cast<uint32_t>((row * kK + bl * 512) * 2));
         }
         constexpr int kPartRow = kNKB * 8;  // partials per h row
         const buf_rsrc pr = make_rsrc(p.act_neg, static_cast<uint32_t>(hrows) * kPartRow * 4);
         for (int i = wave; i < npass * 2 * kNKB; i += kVWaves) {  // 64 partials per load, 2 kNKB per pass
           const int pass = i / (2 * kNKB), j = i - pass * 2 * kNKB;
-          const int4 d = early_desc(gpass(Pc + pass));
+          const int4 d = early_desc(Pc + pass);
           const int base = d.x < 0 ? p.T * p.top_k : d.y;
           const int f = 64 * j + lane, rr = f / kPartRow;
           const int row = base + min(d.w + rr, d.z - 1);
           dma4(pr, lds_hpart + pass * 16 * kPartRow + 64 * j,
-               static_cast<uint32_t>((row * kPartRow + f % kPartRow) * 4), 0, cpol);
+               static_cast<uint32_t>((row * kPartRow + f % kPartRow) * 4), 0);
         }
       }
       wait_vmem();
@@ -935,7 +892,7 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
         __syncthreads();
       }
       staged = true;
-      if (Pc == P_first && !vp.fused) tl_mark(kMode, 2);
+      if (Pc == P_first) tl_mark(kMode, 2);
 
       // compute state of the current unit
       int c_ur = -1, P = 0, a_off = 0;
@@ -1017,9 +974,9 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
         }
       }
     }
-    if (!vp.fused) tl_mark(kMode, 4 + wave, true);
+    tl_mark(kMode, 4 + wave, true);
     lds_barrier();  // partial sums of split units are in LDS
-    if (!vp.fused) tl_mark(kMode, 12);
+    tl_mark(kMode, 12);
     if (head_unit >= 0) {
       // sum the partials of the waves before this one that share the unit, in wave order
       const int gs = head_unit * kNKB;
@@ -1039,104 +996,198 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
   }
 }
 
+// Lane quarters <-> words: word D of lane quarter Q becomes word Q of lane quarter D (a 4 x 4
+// transpose of four 32-bit words across the wave's four 16-lane quarters).  permlane32_swap
+// exchanges the upper 32 lanes of its first operand with the lower 32 of its second,
+// permlane16_swap the odd 16-lane rows of the first with the even rows of the second.
+__device__ __forceinline__ void quarter_transpose(uint32_t (&w)[4]) {
+  auto s02 = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+  auto s13 = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+  auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+  auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+  w[0] = s01[0];
+  w[1] = s01[1];
+  w[2] = s23[0];
+  w[3] = s23[1];
+}
+
+// Split-K down GEMM of a routing gate/up launch (VerifyParams::fuse_down): after its gate/up
+// units, this workgroup holds h for its unit range in LDS -- strips [sa, sb) of at most two
+// passes -- and multiplies each pass's rows by the matching K-slice of the down bank, so the
+// down weights stream inside this launch and no h leaves it.  Work item = one 32-column
+// quarter q of I (two strips) for all of this wave's H / 128 output tiles: per group of 4
+// tiles one 16-byte load per lane (lane quarter Q: tile 4g + Q, its row lane % 16, the
+// quarter's 32 k; contiguous 256 bytes per 16 lanes in the tiled layout), transposed so lane
+// l holds k-octet l / 16 of each tile's row l % 16 -- the B operand of one
+// v_mfma_f32_16x16x32_bf16 per tile -- against the quarter's h fragment; each tile's result is
+// scaled by its group scale and summed over the quarters.  Quarters half inside the range
+// read zero h for the missing strip.  The sums are this workgroup's partial y rows (fp32,
+// unweighted) at 16-row segment b + P; the combine adds every workgroup's partial of a row.
+template <int kN4, typename ScaleT>
+__device__ __forceinline__ void fused_down(const VerifyParams& vp, char* lds, const int total_passes) {
+  // an item is one quarter for one group of 4 tiles; a quarter's kN4 items are consecutive, so
+  // with kQD a multiple of kN4 an item's group is a compile-time index of the unrolled ring
+  constexpr int kQD = kN4 == 4 ? 8 : 6;  // items in flight per wave (one 16-byte load per lane each)
+  static_assert(kQD % kN4 == 0, "ring depth must hold whole quarters");
+  const int strips = vp.g.strips;
+  const int64_t U = static_cast<int64_t>(total_passes) * strips;
+  const int G = static_cast<int>(gridDim.x), b = static_cast<int>(blockIdx.x);
+  const int ub = static_cast<int>(U * b / G), ue = static_cast<int>(U * (b + 1) / G);
+  if (ue <= ub) return;
+  const int I = vp.dI, H = vp.dH, nq = I >> 5, nbq = I >> 7;  // quarters per row, 128-column blocks
+  const int ngd = I / vp.dG, qshift = vp.dG == 256 ? 3 : 2;     // groups per row; quarter -> group
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = lane_id(), lr = lane & 15, kq = lane >> 4;
+  const uint16_t* lh = reinterpret_cast<const uint16_t*>(lds + vp.lds_h);  // [2][16][I]
+  float* lst = reinterpret_cast<float*>(lds + vp.lds_hstart);            // [2][nq][16]
+  const int4* lds_pdesc = reinterpret_cast<const int4*>(lds + vp.lds_pdesc);
+  const int P0 = ub / strips, np = (ue - 1) / strips - P0 + 1;           // 1 or 2 pass slots
+
+  // quarter ranges and descriptors of the slots (scalars: an array indexed by the runtime
+  // slot would live in scratch memory)
+  auto wave_desc = [&](int P) {
+    const int4 v = lds_pdesc[P];
+    return make_int4(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
+                     __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w));
+  };
+  const int sa0 = ub - P0 * strips, sb0 = min(ue, (P0 + 1) * strips) - P0 * strips;
+  const int qa0 = sa0 >> 1, qb0 = (sb0 + 1) >> 1;
+  const int qb1 = np > 1 ? (ue - (P0 + 1) * strips + 1) >> 1 : 0;  // slot 1 starts at quarter 0
+  const int4 dsc0 = wave_desc(P0), dsc1 = wave_desc(P0 + np - 1);
+  const int n0 = qb0 - qa0, nQ = n0 + qb1, nI = nQ * kN4;
+
+  // Loads of item i (clamped: past the end they repeat the last one, never computed).  Tiled:
+  // the quarter of a tile is 256 contiguous bytes (16 rows x 16 bytes); portable: 16 bytes of
+  // each row, rows I / 2 bytes apart (correct, but a row's 128-byte line serves 8 quarters).
+  const bool tiled = vp.g.tiled != 0;
+  const uint32_t tile_bytes = static_cast<uint32_t>(nbq) * 1024u, rowb = static_cast<uint32_t>(I) / 2u;
+  const uint32_t wlane = tiled ? static_cast<uint32_t>(kq) * tile_bytes + static_cast<uint32_t>(lr) * 16u
+                               : static_cast<uint32_t>(16 * kq + lr) * rowb;
+  const int tile0 = wave * 4 * kN4;  // this wave's first output tile (16 rows of H)
+  struct Item {
+    uint4 w;
+    uint32_t s[4];
+  };
+  auto issue = [&](Item& it, int i) {
+    i = max(min(i, nI - 1), 0);
+    const int Q = i / kN4, g = i - Q * kN4;
+    const bool j0 = Q < n0;
+    const int q = j0 ? qa0 + Q : Q - n0;
+    const int4 d = j0 ? dsc0 : dsc1;
+    const bool shared = d.x < 0;
+    const uint8_t* wb = shared ? vp.dw_shared : vp.dw + static_cast<int64_t>(d.x) * vp.dw_stride;
+    const ScaleT* sb = static_cast<const ScaleT*>(shared ? vp.ds_shared : vp.ds) +
+                       (shared ? 0 : static_cast<int64_t>(d.x) * vp.ds_stride);
+    const buf_rsrc wr = make_rsrc(wb, static_cast<uint32_t>(H) * static_cast<uint32_t>(I) / 2);
+    const uint32_t qoff = tiled ? static_cast<uint32_t>(q >> 2) * 1024u + static_cast<uint32_t>(q & 3) * 256u
+                                : static_cast<uint32_t>(q) * 16u;
+    const uint32_t t0 = static_cast<uint32_t>(tile0 + 4 * g);
+    it.w = buf_load16(wr, wlane, (tiled ? t0 * tile_bytes : t0 * 16u * rowb) + qoff);
+    const int gq = q >> qshift;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int64_t tile = tile0 + 4 * g + t;
+      it.s[t] = load_scale_bits(sb + (tiled ? (tile * ngd + gq) * 16 + lr : (tile * 16 + lr) * ngd + gq));
+    }
+  };
+  Item ring[kQD];
+#pragma unroll
+  for (int i = 0; i + 1 < kQD; ++i) issue(ring[i], i);
+
+  // every h value of the range is in LDS (the gate/up epilogues); -136 * sum per quarter and row
+  lds_barrier();
+  for (int i = threadIdx.x; i < 2 * nq * 16; i += kVThreads) {
+    const int r = i & 15, q = (i >> 4) % nq, j = i / (16 * nq);
+    const uint4* src = reinterpret_cast<const uint4*>(lh + (j * 16 + r) * I + 32 * q);
+    float sum = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint4 v = src[c];
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int h2 = 0; h2 < 4; ++h2) sum += __uint_as_float(w[h2] << 16) + __uint_as_float(w[h2] & 0xFFFF0000u);
+    }
+    lst[(j * nq + q) * 16 + r] = -kDequantOffset * sum;
+  }
+  lds_barrier();
+
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  f32x4 tot[kN4][4];
+#pragma unroll
+  for (int g = 0; g < kN4; ++g)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) tot[g][t] = zero;
+  // this wave's partial y rows of slot j: rows 4 kq + e of its tiles' column lr
+  auto flush = [&](int j) {
+    const int4 d = j == 0 ? dsc0 : dsc1;
+    const int64_t row0 = static_cast<int64_t>(vp.part_rps) * (b + P0 + j);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int r = 4 * kq + e;
+      if (d.w + r < d.z) {
+        float* o = vp.ypart + (row0 + r) * H + tile0 * 16 + lr;
+#pragma unroll
+        for (int g = 0; g < kN4; ++g)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) o[(4 * g + t) * 16] = tot[g][t][e];
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < kN4; ++g)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) tot[g][t] = zero;
+  };
+  int cur = 0;
+  uint4 a = make_uint4(0u, 0u, 0u, 0u);
+  f32x4 start = zero;
+  for (int i0 = 0; i0 < nI; i0 += kQD) {
+#pragma unroll
+    for (int u = 0; u < kQD; ++u) {
+      const int i = i0 + u;
+      issue(ring[(u + kQD - 1) % kQD], i + kQD - 1);
+      if (i < nI) {
+        const int g = u % kN4;  // == i % kN4: i0 is a multiple of kQD, a multiple of kN4
+        if (g == 0) {           // first item of a quarter: its slot, h fragment and start terms
+          const int Q = i / kN4;
+          const int j = Q < n0 ? 0 : 1;
+          if (j != cur) {
+            flush(cur);
+            cur = j;
+          }
+          const int q = j == 0 ? qa0 + Q : Q - n0;
+          a = *reinterpret_cast<const uint4*>(lh + (j * 16 + lr) * I + 32 * q + 8 * kq);
+          start = *reinterpret_cast<const f32x4*>(lst + (j * nq + q) * 16 + 4 * kq);
+        }
+        const Item& it = ring[u];
+        uint32_t w[4] = {it.w.x, it.w.y, it.w.z, it.w.w};
+        quarter_transpose(w);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const f32x4 acc = mfma16x16x32(a, dequant8(w[t]), start);
+          tot[g][t] += scale_value<ScaleT>(it.s[t]) * acc;
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  flush(cur);
+}
+
 template <int kMode, int kNKB, typename ScaleT>
 __global__ __launch_bounds__(512) void w4_verify_kernel(VerifyParams vp) {
   __shared__ __attribute__((aligned(16))) char lds[kVLds];
   tl_mark(kMode, 0);
   const int total_passes = verify_passes<kMode, kNKB>(vp, lds);
   tl_mark(kMode, 1);
-  verify_gemm<kMode, kNKB, ScaleT>(vp, lds, total_passes,
-                                   Split{0, 1, static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x)});
+  verify_gemm<kMode, kNKB, ScaleT>(vp, lds, total_passes);
+  if constexpr (kMode == kModeGateUp) {
+    if (vp.fuse_down) fused_down<kNKB / 4, ScaleT>(vp, lds, total_passes);
+  }
 #ifdef DFLASH_TIMELINE
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   tl_mark(kMode, 13);
 #endif
-}
-
-// After gate/up range `rank` of part `part` (the split verify_gemm made): every store of the
-// workgroup has reached the XCD's L2 (stores are acknowledged there; L1 writes through), then
-// each pass the range touched gets the number of its units the range finished added to its
-// count, which the down ranges of the part poll.  The workgroup's LDS is free afterwards.
-__device__ __forceinline__ void publish_ready(const VerifyParams& vp, int total_passes, int part, int rank,
-                                              int ranks) {
-  __builtin_amdgcn_s_waitcnt(0);  // this thread's h and partial stores are acknowledged by L2
-  __syncthreads();
-  const int strips = vp.g.strips;
-  const int local_passes = total_passes > part ? (total_passes - part + kXcds - 1) / kXcds : 0;
-  const int64_t total_units = static_cast<int64_t>(local_passes) * strips;
-  const int ub = static_cast<int>(total_units * rank / ranks), ue = static_cast<int>(total_units * (rank + 1) / ranks);
-  if (ue > ub) {
-    for (int j = ub / strips + static_cast<int>(threadIdx.x); j <= (ue - 1) / strips; j += kVThreads) {
-      const int n = min(ue, (j + 1) * strips) - max(ub, j * strips);
-      __hip_atomic_fetch_add(ready_word(vp, part, j), n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-  __syncthreads();
-}
-
-// After the workgroup's last claim came back empty (every wait of it has ended): the last
-// workgroup of the grid to get here knows every range of every part finished, and returns
-// all counts, queues and the done count to zero for the next launch on this workspace.
-__device__ __forceinline__ void reset_ready(const VerifyParams& vp, int* lds_flag) {
-  if (threadIdx.x == 0)
-    *lds_flag = __hip_atomic_fetch_add(vp.done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                static_cast<int>(gridDim.x) - 1;
-  __syncthreads();
-  if (*lds_flag) {
-    for (int i = static_cast<int>(threadIdx.x); i < kXcds * vp.ready_stride; i += kVThreads)
-      __hip_atomic_store(vp.ready + i, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (threadIdx.x == 0) __hip_atomic_store(vp.done, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-}
-
-// The routed-MoE layer's expert FFN in one launch: routing prologue, gate/up, then down.  Pass
-// P belongs to part P % 8 in both phases, and only workgroups running on XCD P % 8 (read from
-// the hardware, whatever the dispatch order) take ranges of it, so a down range waits only on
-// gate/up work of its own XCD: counts and h rows meet in that XCD's L2, and nothing crosses
-// XCDs inside the launch.  The combine that sums each token's slots over all XCDs stays a
-// launch of its own.  Ranges are claimed from the part's queues (gate/up first, then down,
-// the next claim in flight during a range), so a part's gate/up ranges all go to workgroups
-// that finish them before any down range of theirs: every wait ends once each XCD runs a
-// workgroup, whatever the residency, and a wait that does not end gives up after its budget.
-template <int kNKBg, int kNKBd, typename ScaleT>
-__global__ __launch_bounds__(512) void w4_layer_kernel(VerifyParams gu, VerifyParams dn) {
-  __shared__ __attribute__((aligned(16))) char lds[kVLds];
-  __shared__ int bcast;
-  const int tid = threadIdx.x;
-  const int part = static_cast<int>(xcc_id());
-  if (part >= kXcds) {  // not an 8-XCD device: take no range (the waits of the others give up)
-    if (tid == 0) __hip_atomic_fetch_or(gu.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    reset_ready(gu, &bcast);
-    return;
-  }
-  // thread 0 claims; the value reaches the workgroup through LDS
-  auto claim = [&](int phase) {
-    return __hip_atomic_fetch_add(queue_word(gu, part, phase), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  };
-  auto share = [&](int v) {
-    if (tid == 0) bcast = v;
-    __syncthreads();
-    const int c = bcast;
-    __syncthreads();
-    return c;
-  };
-  int next_gu = 0, next_dn = 0;
-  if (tid == 0) {  // both first claims travel during the routing prologue
-    next_gu = claim(0);
-    next_dn = claim(1);
-  }
-  const int total_passes = verify_passes<kModeGateUp, kNKBg>(gu, lds);
-  for (int c = share(next_gu); c < gu.chunks; c = share(next_gu)) {
-    if (tid == 0) next_gu = claim(0);
-    verify_gemm<kModeGateUp, kNKBg, ScaleT>(gu, lds, total_passes, Split{part, kXcds, c, gu.chunks});
-    publish_ready(gu, total_passes, part, c, gu.chunks);
-  }
-  for (int c = share(next_dn); c < dn.chunks; c = share(next_dn)) {
-    if (tid == 0) next_dn = claim(1);
-    verify_gemm<kModeDown, kNKBd, ScaleT>(dn, lds, total_passes, Split{part, kXcds, c, dn.chunks});
-  }
-  reset_ready(gu, &bcast);
 }
 
 // ---------------------------------------------------------------------------
@@ -1221,7 +1272,7 @@ bool verify_layout(int mode, int T, int K, int N, int E, int k, int has_shared, 
   const int base = off;
   const int tpad = (T + 3) & ~3;
   const int scratch = al(((E + 3) & ~3) * 4) + al(((T * k + 3) & ~3) * 4) + 96 + E * tpad;
-  const int row_scratch = (256 + 512 + 512 + 12) * 4 + E * tpad;  // route_rows: counts, weights, ids, totals, map
+  const int row_scratch = (256 + 512 + 512 + 12 + 256) * 4 + E * tpad;  // route_rows: counts, weights, ids, totals, first passes, map
   if (route && E <= 256 && k <= 16 && T * k <= 512 && base + std::max(part, row_scratch) <= kVLds) {
     L.route = 2;
     L.lds_part = L.lds_scratch = take(std::max(part, row_scratch));
@@ -1236,6 +1287,17 @@ bool verify_layout(int mode, int T, int K, int N, int E, int k, int has_shared, 
   return mode == kModeGateUp && gather_layout();  // whole-block plan too large: gathered chunks
 }
 
+
+int fused_down_lds(int I) { return ((2 * 16 * I * 2 + 15) & ~15) + ((2 * (I / 32) * 16 * 4 + 15) & ~15); }
+
+bool fused_down_layout(VerifyParams* vp, int I) {
+  const int off = (vp->lds_bytes + 15) & ~15;
+  if (vp->route != 2 || off + fused_down_lds(I) > kVLds) return false;
+  vp->lds_h = off;
+  vp->lds_hstart = off + ((2 * 16 * I * 2 + 15) & ~15);
+  vp->lds_bytes = off + fused_down_lds(I);
+  return true;
+}
 
 void launch_w4_verify(int mode, bool fp32_scales, int grid, const VerifyParams& vp, hipStream_t stream) {
   const dim3 g(static_cast<unsigned>(grid)), blk(kVThreads);
@@ -1260,88 +1322,6 @@ void launch_w4_verify(int mode, bool fp32_scales, int grid, const VerifyParams& 
   }
 #undef DFLASH_VERIFY_K
 #undef DFLASH_VERIFY
-}
-
-bool layer_layout(int T, int H, int I, int E, int k, int has_shared, VerifyParams* gu, VerifyParams* dn) {
-  // instantiated shapes: gate/up over H in {512, 1024, 2048}, down over I in {512, 1024}
-  if ((H != 512 && H != 1024 && H != 2048) || (I != 512 && I != 1024)) return false;
-  if (T <= 0 || T > 32 || k <= 0 || H % kVStrip) return false;
-  auto al = [](int v) { return (v + 15) & ~15; };
-  const int part = kVWaves * 2 * 64 * 16;
-  int off = 0;
-  auto take = [&](int bytes) {
-    const int o = off;
-    off += al(bytes);
-    return o;
-  };
-  // shared by both phases: every pass descriptor and the token of every slot row (routing)
-  const int tpasses = (T + 15) / 16;
-  const int pd_cap = std::min(E, T * k) * tpasses + (has_shared ? tpasses : 0);
-  const int pdesc = take(pd_cap * 16), tok = take(T * k * 4);
-  const int u0 = off;
-  // gate/up phase: all T x rows, their -136*sum terms, the routing scratch / split partials
-  *gu = VerifyParams{};
-  const int rs_g = 2 * H + 16, nkb_g = H / 128;
-  gu->a_rows = T;
-  gu->pd_cap = pd_cap;
-  gu->lds_pdesc = pdesc;
-  gu->lds_tok = tok;
-  gu->lds_a = take(T * rs_g);
-  gu->lds_neg = take(((T * nkb_g + 63) & ~63) * 4);
-  const int tpad = (T + 3) & ~3;
-  const int row_scratch = (256 + 512 + 512 + 12) * 4 + E * tpad;
-  const int scratch = al(((E + 3) & ~3) * 4) + al(((T * k + 3) & ~3) * 4) + 96 + E * tpad;
-  if (E <= 256 && k <= 16 && T * k <= 512) {
-    gu->route = 2;
-    gu->lds_part = gu->lds_scratch = take(std::max(part, row_scratch));
-  } else if (E <= 2 * kVThreads) {
-    gu->route = 1;
-    gu->lds_part = gu->lds_scratch = take(std::max(part, al(scratch)));
-  } else {
-    return false;
-  }
-  gu->lds_bytes = off;
-  if (off > kVLds) return false;
-  // down phase over the same bytes after the descriptors: chunks of h rows and their partials
-  off = u0;
-  *dn = VerifyParams{};
-  const int rs_d = 2 * I + 16, nkb_d = I / 128;
-  dn->lds_part = dn->lds_scratch = take(part);
-  const int per_pass = 16 * rs_d + al(16 * nkb_d * 4) + al(16 * nkb_d * 8 * 4);
-  const int cp = std::min(8, (kVLds - off) / per_pass);
-  if (cp < 1) return false;
-  dn->chunk_passes = cp;
-  dn->pd_cap = pd_cap;
-  dn->a_rows = cp * 16;
-  dn->lds_pdesc = pdesc;
-  dn->lds_tok = tok;
-  dn->lds_a = take(cp * 16 * rs_d);
-  dn->lds_neg = take(cp * 16 * nkb_d * 4);
-  dn->lds_wgt = take(cp * 16 * nkb_d * 8 * 4);
-  dn->lds_bytes = off;
-  gu->fused = dn->fused = 1;
-  return off <= kVLds;
-}
-
-void launch_w4_layer(bool fp32_scales, int grid, const VerifyParams& gu, const VerifyParams& dn, hipStream_t stream) {
-  const dim3 g(static_cast<unsigned>(grid)), blk(kVThreads);
-#define DFLASH_LAYER(NG, ND)                                                                             \
-  do {                                                                                                   \
-    if (fp32_scales) hipLaunchKernelGGL((w4_layer_kernel<NG, ND, float>), g, blk, 0, stream, gu, dn);   \
-    else hipLaunchKernelGGL((w4_layer_kernel<NG, ND, uint16_t>), g, blk, 0, stream, gu, dn);            \
-  } while (0)
-#define DFLASH_LAYER_D(NG)                            \
-  do {                                                \
-    if (dn.g.K == 512) DFLASH_LAYER(NG, 4);           \
-    else DFLASH_LAYER(NG, 8);                         \
-  } while (0)
-  switch (gu.g.K) {
-    case 512: DFLASH_LAYER_D(4); break;
-    case 1024: DFLASH_LAYER_D(8); break;
-    default: DFLASH_LAYER_D(16); break;
-  }
-#undef DFLASH_LAYER_D
-#undef DFLASH_LAYER
 }
 
 #ifdef DFLASH_TIMELINE

@@ -365,21 +365,19 @@ def moe_workspace_bytes(tokens: int, hidden: int, inter: int, experts: int, top_
                                                       int(has_shared)))
 
 
-def set_fused_layer(enable: bool) -> None:
-    """Process-wide: run a verify block's gate/up and down as one launch where it fits (off by default)."""
-    _lib.call("dflash_set_fused_layer", int(bool(enable)))
+def set_split_down(enable: bool) -> None:
+    """Process-wide: run a verify block's down GEMM inside its gate/up launch where it fits
+    (on by default; off runs the separate down launch, for comparisons)."""
+    _lib.call("dflash_set_split_down", int(bool(enable)))
 
 
-def moe_fused_status_offset(tokens: int, hidden: int, inter: int, experts: int, top_k: int, group_size: int,
-                            has_shared: bool) -> int:
-    """Byte offset in a moe_w4a16 workspace of the one-launch expert FFN's status word, or -1.
-
-    -1 means a layer of this shape runs gate/up and down as separate launches.
-    After a call the word is 0, or has bit 0 (a workgroup ran on another XCD) or
-    bit 1 (a wait for gate/up rows gave up) set.  Needs the current device.
-    """
-    return int(_lib.load().dflash_moe_fused_status_offset(tokens, hidden, inter, experts, top_k, group_size,
-                                                          int(has_shared)))
+def moe_split_down(tokens: int, hidden: int, inter: int, experts: int, top_k: int, group_size: int,
+                   has_shared: bool, scale_dtype: torch.dtype = torch.bfloat16, layout: str = "tiled") -> bool:
+    """Whether a ``moe_w4a16`` call of this shape runs the split-K down on the current device."""
+    return bool(_lib.load().dflash_moe_split_down(
+        tokens, hidden, inter, experts, top_k, group_size, int(has_shared),
+        _lib.DTYPE_F32 if scale_dtype == torch.float32 else _lib.DTYPE_BF16,
+        _lib.LAYOUT_TILED if layout == "tiled" else _lib.LAYOUT_PORTABLE))
 
 
 STAGE_GATE_UP = _lib.STAGE_GATE_UP

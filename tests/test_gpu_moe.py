@@ -203,14 +203,24 @@ def test_moe_repeat_calls_are_identical(pkg, device):
     assert torch.equal(a, b)
 
 
+@pytest.fixture
+def two_launches(pkg):
+    """The verify block's down GEMM as a launch of its own for one test (the split-K down off)."""
+    pkg.ops.set_split_down(False)
+    try:
+        yield
+    finally:
+        pkg.ops.set_split_down(True)
+
+
 @pytest.mark.parametrize("tokens", [16, 40, 128])
-def test_measure_stage_relaunches_one_kernel(pkg, device, tokens):
+def test_measure_stage_relaunches_one_kernel(pkg, device, tokens, two_launches):
     """Measurement mode re-runs one stage on the workspace of a full call and rewrites identical
     bytes (gate/up and down as separate launches: verify block, gathered verify, T=128)."""
     layer = pkg.synthetic.moe_layer(tokens, seed=6)
     gu, dn, sh = _to(pkg, layer, device)
     x, rw = layer.hidden.to(device), layer.router_weight.to(device)
-    assert pkg.ops.moe_fused_status_offset(tokens, 2048, 512, 256, 8, 128, True) == -1
+    assert not pkg.ops.moe_split_down(tokens, 2048, 512, 256, 8, 128, True)
     ws = torch.empty(pkg.ops.moe_workspace_bytes(tokens, 2048, 512, 256, 8, 128, True), dtype=torch.uint8,
                      device=device)
     ref = pkg.ops.moe_w4a16(x, gu, dn, top_k=8, router_weight=rw, shared=sh, workspace=ws)
@@ -228,30 +238,19 @@ def test_measure_stage_relaunches_one_kernel(pkg, device, tokens):
     assert torch.equal(again, ref)
 
 
-@pytest.fixture
-def fused_layer(pkg):
-    """The one-launch expert FFN switched on for one test."""
-    pkg.ops.set_fused_layer(True)
-    try:
-        yield
-    finally:
-        pkg.ops.set_fused_layer(False)
-
-
-def test_measure_stage_relaunches_the_fused_kernel(pkg, device, fused_layer):
-    """T=16: measurement of EXPERTS with the call's router logits relaunches the one-launch
-    expert FFN, which rewrites identical bytes (its counts return to zero, its status stays 0)."""
+def test_measure_stage_relaunches_the_split_kernel(pkg, device):
+    """T=16: measurement of EXPERTS with the call's router logits relaunches the gate/up launch
+    that also runs the split-K down, which rewrites identical bytes."""
     layer = pkg.synthetic.moe_layer(16, seed=6)
     gu, dn, sh = _to(pkg, layer, device)
+    gu, dn, sh = gu.tiled(), dn.tiled(), sh.tiled()
+    assert pkg.ops.moe_split_down(16, 2048, 512, 256, 8, 128, True)
     x, rw = layer.hidden.to(device), layer.router_weight.to(device)
     lg = pkg.ops.router_logits(x, rw)
-    status = pkg.ops.moe_fused_status_offset(16, 2048, 512, 256, 8, 128, True)
-    assert status > 0
     ws = torch.empty(pkg.ops.moe_workspace_bytes(16, 2048, 512, 256, 8, 128, True), dtype=torch.uint8, device=device)
     ref = pkg.ops.moe_w4a16(x, gu, dn, top_k=8, router_logits=lg, shared=sh, workspace=ws)
     torch.cuda.synchronize()
     snapshot = ws.clone()
-    assert int(snapshot[status:status + 4].view(torch.int32).item()) == 0
     pkg.ops.set_measure_stage(pkg.ops.STAGE_EXPERTS)
     try:
         for _ in range(3):
@@ -264,58 +263,63 @@ def test_measure_stage_relaunches_the_fused_kernel(pkg, device, fused_layer):
     assert torch.equal(again, ref)
 
 
-def _fused_words(ws, status, tokens, k):
-    """The one-launch FFN's words: per XCD a block of stride words (counts of its at most
-    ceil((T*k + T) / 8) passes, then its two queues; 128-byte lines), a line holding the
-    done count, then the status word."""
-    local = (tokens * k + tokens + 7) // 8
-    stride = (local + 2 + 31) // 32 * 32
-    return ws[status - 4 * (8 * stride + 32):status + 4].view(torch.int32).cpu()
-
-
-@pytest.mark.parametrize("tokens,experts,k,hidden,inter,group,scale_dtype,shared", [
-    (16, 256, 8, 2048, 512, 128, torch.bfloat16, True),     # the verify block
-    (1, 256, 8, 2048, 512, 128, torch.bfloat16, True),      # one token: most XCDs get no pass
-    (32, 64, 8, 2048, 1024, 256, torch.float32, True),      # largest T, down over K = 1024, group 256
-    (7, 512, 4, 1024, 512, 128, torch.bfloat16, False),     # block routing (E > 256), no shared expert
+@pytest.mark.parametrize("tokens,experts,k,hidden,inter,group,scale_dtype,shared,layout", [
+    (16, 256, 8, 2048, 512, 128, torch.bfloat16, True, "tiled"),      # the verify block
+    (16, 256, 8, 2048, 512, 128, torch.bfloat16, True, "portable"),
+    (1, 256, 8, 2048, 512, 128, torch.bfloat16, True, "tiled"),       # one token: a pass spans ~28 workgroups
+    (5, 64, 4, 1024, 1024, 256, torch.float32, True, "tiled"),        # down over K = 1024, group 256, fp32 scales
+    (24, 16, 4, 1024, 512, 128, torch.bfloat16, True, "tiled"),       # full 16-row passes, two shared passes
+    (16, 32, 2, 512, 512, 128, torch.bfloat16, False, "tiled"),       # H = 512, no shared expert
 ])
-def test_fused_layer_launch(pkg, device, fused_layer, tokens, experts, k, hidden, inter, group, scale_dtype, shared):
-    """Gate/up and down in one launch: the shape runs fused; over three calls in a row on one
-    workspace (the last with fewer tokens) every output meets the oracle bar and matches the
-    two-launch output to within the order of fp32 sums, the status word reads 0, and every
-    count and queue is back at zero after the call."""
-    print(f"fused layer T={tokens} E={experts} k={k} H={hidden} I={inter} g={group}", flush=True)
+def test_split_down_layer(pkg, device, tokens, experts, k, hidden, inter, group, scale_dtype, shared, layout):
+    """The down GEMM inside the gate/up launch (split over K by each workgroup's strips, partial
+    rows added by the combine): on one workspace, a call, a repeat and a smaller block after it
+    each route bit-exactly, meet the oracle bar, repeat bit-identically, and agree with the two
+    launches to within the fp32 summation order."""
     ws = torch.empty(pkg.ops.moe_workspace_bytes(tokens, hidden, inter, experts, k, group, shared),
                      dtype=torch.uint8, device=device)
-    for t in (tokens, tokens, max(1, tokens // 2)):
-        status = pkg.ops.moe_fused_status_offset(t, hidden, inter, experts, k, group, shared)
-        assert status > 0, t
+    prev = None
+    for t in (tokens, tokens, max(1, tokens // 3)):
+        print(f"split down T={t} E={experts} k={k} H={hidden} I={inter} g={group} {layout}", flush=True)
+        assert pkg.ops.moe_split_down(t, hidden, inter, experts, k, group, shared, scale_dtype, layout)
         layer = pkg.synthetic.moe_layer(t, hidden=hidden, inter=inter, experts=experts, group_size=group,
                                         seed=t + 3 * experts, shared=shared, scale_dtype=scale_dtype)
         gu, dn, sh = _to(pkg, layer, device)
-        out, r, logits = pkg.ops.moe_w4a16(layer.hidden.to(device), gu.tiled(), dn.tiled(), top_k=k,
-                                           router_weight=layer.router_weight.to(device),
-                                           shared=sh.tiled() if sh else None, return_routing=True, workspace=ws)
-        torch.cuda.synchronize()
-        words = _fused_words(ws, status, t, k)
-        assert int(words[-1]) == 0, f"status {int(words[-1])}"
-        assert int(words[:-1].abs().sum()) == 0
-        pkg.ops.set_fused_layer(False)
+        if layout == "tiled":
+            gu, dn, sh = gu.tiled(), dn.tiled(), sh.tiled() if sh else None
+        x, rw = layer.hidden.to(device), layer.router_weight.to(device)
+        out, r, logits = pkg.ops.moe_w4a16(x, gu, dn, top_k=k, router_weight=rw, shared=sh, return_routing=True,
+                                           workspace=ws)
+        if prev is not None and prev[0] == t:
+            assert torch.equal(out, prev[1])
+        prev = (t, out.clone())
+        pkg.ops.set_split_down(False)
         try:
-            assert pkg.ops.moe_fused_status_offset(t, hidden, inter, experts, k, group, shared) == -1
-            two = pkg.ops.moe_w4a16(layer.hidden.to(device), gu.tiled(), dn.tiled(), top_k=k,
-                                    router_weight=layer.router_weight.to(device),
-                                    shared=sh.tiled() if sh else None)
+            two = pkg.ops.moe_w4a16(x, gu, dn, top_k=k, router_weight=rw, shared=sh)
         finally:
-            pkg.ops.set_fused_layer(True)
-        assert metrics.compare(out.cpu(), two.float().cpu().numpy())["max_rel"] <= 1e-2
+            pkg.ops.set_split_down(True)
         ogu, odn, osh = _oracle_banks(layer)
         golden = oracle_moe.moe(layer.hidden, logits.cpu().numpy(), k, ogu, odn, group, shared=osh)
         np.testing.assert_array_equal(r.ids.cpu().numpy(), golden["ids"])
         np.testing.assert_array_equal(r.perm.cpu().numpy(), golden["perm"])
+        np.testing.assert_array_equal(r.inv.cpu().numpy(), golden["inv"])
+        np.testing.assert_array_equal(r.offsets.cpu().numpy(), golden["offsets"])
         report = metrics.compare(out.cpu(), golden["out_f32"])
-        print(f"  T={t} report={report}", flush=True)
+        versus = metrics.compare(out.cpu(), two.float().cpu().numpy())
+        print(f"  T={t} report={report} vs two launches max_rel={versus['max_rel']:.2e}", flush=True)
         assert report["max_rel"] <= TOL and report["cosine"] > 0.9999, report
+        assert versus["max_rel"] <= 4e-3, versus
+
+
+def test_split_down_refused_shapes_run_two_launches(pkg, device):
+    """Shapes outside the split-K down -- unit ranges of more than two passes (T=32 at E=256,
+    top-8), H outside {512, 1024, 2048}, blocks routed outside the gate/up launch -- run the
+    separate down launch and still meet the oracle bar."""
+    assert not pkg.ops.moe_split_down(32, 2048, 512, 256, 8, 128, True)
+    assert not pkg.ops.moe_split_down(16, 1536, 512, 64, 8, 128, True)
+    assert not pkg.ops.moe_split_down(40, 2048, 512, 256, 8, 128, True)
+    layer = pkg.synthetic.moe_layer(32, seed=77)
+    _run_and_check(pkg, device, layer, 8)
 
 
 def test_empty_batch(pkg, device):
