@@ -200,8 +200,8 @@ class OriginalShards:
         packed by ``dflash_w4_from_int8`` (its range checks raise the reader's ``ValueError``s)."""
         meta = self.describe(key, shape)
         weight, scale = self._map(meta["weight"]), self._map(meta["scale"])
-        values = torch.from_numpy(np.ascontiguousarray(weight)).to(device)
-        scales = torch.from_numpy(np.ascontiguousarray(scale)).to(device)
+        values = torch.from_numpy(np.array(weight, copy=True)).to(device)   # the maps are read-only
+        scales = torch.from_numpy(np.array(scale, copy=True)).to(device)
         self._unchanged((meta["weight"]["shard"], meta["scale"]["shard"]))
         return ops.from_int8(values, scales, ORIGINAL_GROUP_SIZE, layout=layout)
 

@@ -1033,14 +1033,26 @@ __device__ __forceinline__ void fused_down(const VerifyParams& vp, char* lds, co
   const int64_t U = static_cast<int64_t>(total_passes) * strips;
   const int G = static_cast<int>(gridDim.x), b = static_cast<int>(blockIdx.x);
   const int ub = static_cast<int>(U * b / G), ue = static_cast<int>(U * (b + 1) / G);
-  if (ue <= ub) return;
+  const int4* lds_pdesc = reinterpret_cast<const int4*>(lds + vp.lds_pdesc);
+  if (ue <= ub) {
+    // An empty range (more workgroups than units) strictly inside pass P's units lies between
+    // the pass's first and last workgroups, whose partial rows the combine adds one by one:
+    // it writes zero rows.  (An empty range at a pass boundary belongs to no pass's run.)
+    const int P = ub / strips;
+    if (ub < U && ub != P * strips) {
+      const int4 d = lds_pdesc[P];
+      const int rows = min(16, d.z - d.w), quads = vp.dH >> 2;
+      float4* o = reinterpret_cast<float4*>(vp.ypart + static_cast<int64_t>(vp.part_rps) * (b + P) * vp.dH);
+      for (int i = threadIdx.x; i < rows * quads; i += kVThreads) o[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    return;
+  }
   const int I = vp.dI, H = vp.dH, nq = I >> 5, nbq = I >> 7;  // quarters per row, 128-column blocks
   const int ngd = I / vp.dG, qshift = vp.dG == 256 ? 3 : 2;     // groups per row; quarter -> group
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = lane_id(), lr = lane & 15, kq = lane >> 4;
   const uint16_t* lh = reinterpret_cast<const uint16_t*>(lds + vp.lds_h);  // [2][16][I]
   float* lst = reinterpret_cast<float*>(lds + vp.lds_hstart);            // [2][nq][16]
-  const int4* lds_pdesc = reinterpret_cast<const int4*>(lds + vp.lds_pdesc);
   const int P0 = ub / strips, np = (ue - 1) / strips - P0 + 1;           // 1 or 2 pass slots
 
   // quarter ranges and descriptors of the slots (scalars: an array indexed by the runtime
