@@ -12,20 +12,20 @@ multi-layer verify forward would be issued), so host launch overhead is not
 part of the measurement.
 
 Prints ONE JSON line.  ``value`` is microseconds per MoE layer (lower is
-better).  ``roofline`` is the dominant kernel, the layer's one expert launch as
-it runs in the layer: it routes the block in its prologue (from the step's
-router logits), streams the hit experts' gate/up rows, then the matching
-K-slices of their down rows (split-K down, partial y rows for the combine).
-HIP events on its launch stream bracket graph replays that hold only that
-kernel's launches (measurement mode of the library), one per step over the
-same rotation of weight sets and hidden blocks; achieved = its algorithmic
-bytes (int4 gate/up and down rows + bf16 scales of the hit experts and the
-shared expert, x in, partial y rows out) / mean launch duration.
-``traffic`` is the HBM bytes the same kernel moves per launch, from the
-rocprofv3 FETCH_SIZE / WRITE_SIZE passes recorded in
-``profiles/hbm_traffic_split_down_t16.json`` (scaled by the counters' reading
+better).  ``roofline`` is the dominant kernel, the layer's gate/up launch as it
+runs in the layer: it routes the block in its prologue (from the step's router
+logits) and streams the hit experts' gate/up rows.  HIP events on its launch
+stream bracket graph replays that hold only that kernel's launches
+(measurement mode of the library), one per step over the same rotation of
+weight sets and hidden blocks; achieved = its algorithmic bytes (int4 gate/up
+rows + bf16 scales of the hit experts and the shared expert, x in, h out) /
+mean launch duration.  ``traffic`` is the HBM bytes the same kernel moves per
+launch, from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes recorded in
+``profiles/hbm_traffic_gate_up_t16.json`` (scaled by the counters' reading
 of a plain copy of known size), or null when that file is absent.
-``stages`` also times the same layer with the down GEMM as a launch of its own.
+``stages`` times the layer's other expert launches; ``split_down_opt_in`` the
+same layer with the down GEMM inside the gate/up launch (split over K,
+partial y rows added by the combine), which is not the default.
 ``prefill`` reports the T=2048 layer in TFLOP/s against bf16 MFMA peak.
 ``cpu_baseline`` times the oracle's CPU restatement of the same layer.
 """
@@ -370,8 +370,8 @@ def measured_mfma():
 
 
 def measured_traffic():
-    """HBM bytes per T=16 split-K expert launch from the committed counter passes, or None."""
-    path = ROOT / "profiles" / "hbm_traffic_split_down_t16.json"
+    """HBM bytes per T=16 gate/up launch (routing prologue) from the committed counter passes, or None."""
+    path = ROOT / "profiles" / "hbm_traffic_gate_up_t16.json"
     if not path.is_file():
         return None
     rec = json.loads(path.read_text())
@@ -517,30 +517,30 @@ def main() -> int:
     all_bytes = (hits + 1) * (INT4_BYTES_PER_EXPERT + SCALE_BYTES_PER_EXPERT)
     layer_gbs = int4_bytes / (ms * 1e-3) / 1e9
     log("timing the expert kernels with HIP events")
-    # the layer's expert kernel: the gate/up launch that routes the block and runs the split-K
-    # down (measurement of EXPERTS with the step's logits relaunches exactly that kernel)
-    split = pkg.ops.moe_split_down(tokens, 2048, 512, 256, top_k, 128, True)
-    lay_ms, lay_hits, lay_parts = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup,
-                                             pkg.ops.STAGE_EXPERTS, given_logits=True)
-    # the same layer with the down GEMM as a launch of its own, and its two expert kernels alone
-    pkg.ops.set_split_down(False)
-    try:
-        two_layer_ms = time_layer(pkg, sets, blocks, top_k, args.steps, args.warmup, ws)
-        two_ms, _, _ = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup, pkg.ops.STAGE_EXPERTS,
-                                  given_logits=True)
-        gu_ms, gu_hits, _ = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup, given_logits=True)
-        stream_ms, _, _ = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup)
-        dn_ms, _, _ = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup, pkg.ops.STAGE_DOWN)
-    finally:
-        pkg.ops.set_split_down(True)
-    # algorithmic bytes of the split launch: the hit experts' and the shared expert's int4 gate/up
-    # and down rows + bf16 scales, x (bf16) read, the fp32 partial y rows written (h stays in LDS);
-    # of the two-launch form's gate/up launch: gate/up rows + scales, x read, h (bf16) written
+    # the layer's dominant kernel: the gate/up launch that routes the block in its prologue
+    # (measurement of GATE_UP with the step's logits relaunches exactly that kernel), then the
+    # down launch, both together, and the gate/up stream alone (routing given as a work table)
+    gu_ms, gu_hits, _ = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup, given_logits=True)
+    two_ms, _, _ = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup, pkg.ops.STAGE_EXPERTS,
+                              given_logits=True)
+    stream_ms, _, _ = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup)
+    dn_ms, _, _ = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup, pkg.ops.STAGE_DOWN)
+    # the opt-in split-K down (the down GEMM inside the gate/up launch, partial rows added by the
+    # combine): its layer and its one expert kernel
+    log("timing the split-K down form")
+    with pkg.ops.split_down(True):
+        split = pkg.ops.moe_split_down(tokens, 2048, 512, 256, top_k, 128, True)
+        split_layer_ms = time_layer(pkg, sets, blocks, top_k, args.steps, args.warmup, ws)
+        split_ms, split_hits, split_parts = time_stage(pkg, sets, blocks, top_k, args.steps, args.warmup,
+                                                       pkg.ops.STAGE_EXPERTS, given_logits=True)
+    # algorithmic bytes of the gate/up launch: the hit experts' and the shared expert's int4 gate/up
+    # rows + bf16 scales, x (bf16) read, h (bf16) written; of the split launch: gate/up and down
+    # rows + scales, x read, the fp32 partial y rows written (h stays in LDS)
     rows = tokens * top_k + tokens
-    lay_bytes = ((lay_hits + 1) * (GATE_UP_BYTES_PER_EXPERT + DOWN_BYTES_PER_EXPERT) + tokens * 2048 * 2
-                 + lay_parts * 2048 * 4)
     gu_bytes = (gu_hits + 1) * GATE_UP_BYTES_PER_EXPERT + tokens * 2048 * 2 + rows * 512 * 2
-    achieved = lay_bytes / (lay_ms * 1e-3) / 1e9
+    split_bytes = ((split_hits + 1) * (GATE_UP_BYTES_PER_EXPERT + DOWN_BYTES_PER_EXPERT) + tokens * 2048 * 2
+                   + split_parts * 2048 * 4)
+    achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
 
     result = {
         "metric": METRIC, "value": round(ms * 1e3, 2), "unit": "us/layer", "n_gpus": 1,
@@ -557,20 +557,20 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": "w4_verify_kernel<1, 16, unsigned short> (routing prologue + grouped gate/up "
-                               "+ SiLU*up + split-K down, T=16, tiled banks)" if split else
-                               "w4_verify_kernel<1, 16, unsigned short> (routing prologue + grouped gate/up)",
-                     "kernel_us": round(lay_ms * 1e3, 2), "hit_experts_mean": round(lay_hits, 2),
-                     "partial_rows_mean": round(lay_parts, 1), "bytes_per_launch": int(lay_bytes)},
+                               "+ SiLU*up, T=16, tiled banks)",
+                     "kernel_us": round(gu_ms * 1e3, 2), "hit_experts_mean": round(gu_hits, 2),
+                     "bytes_per_launch": int(gu_bytes)},
         "stages": {"expert_stage_us": round(exp_ms * 1e3, 2),
-                   "split_down": bool(split),
-                   "two_launch_layer_us": round(two_layer_ms * 1e3, 2),
-                   "two_launch_expert_kernels_us": round(two_ms * 1e3, 2),
-                   "two_launch_gate_up_us": round(gu_ms * 1e3, 2),
-                   "two_launch_gate_up_gbs": round(gu_bytes / (gu_ms * 1e-3) / 1e9, 1),
-                   "two_launch_down_us": round(dn_ms * 1e3, 2),
+                   "expert_kernels_us": round(two_ms * 1e3, 2),
+                   "gate_up_us": round(gu_ms * 1e3, 2),
+                   "down_us": round(dn_ms * 1e3, 2),
                    "gate_up_stream_only_us": round(stream_ms * 1e3, 2),
                    "expert_int4_bytes": int(int4_bytes), "expert_weight_bytes": int(all_bytes),
                    "expert_stage_int4_gbs": round(int4_bytes / (exp_ms * 1e-3) / 1e9, 1)},
+        "split_down_opt_in": {"runs": bool(split), "layer_us": round(split_layer_ms * 1e3, 2),
+                              "kernel_us": round(split_ms * 1e3, 2),
+                              "kernel_gbs": round(split_bytes / (split_ms * 1e-3) / 1e9, 1),
+                              "partial_rows_mean": round(split_parts, 1), "bytes_per_launch": int(split_bytes)},
     }
     if not args.no_prefill:
         log("timing the T=2048 prefill layer")

@@ -178,8 +178,8 @@ int dflash_moe_experts_w4a16(const void* hidden, int64_t tokens, int64_t hidden_
  * OriginalQuantizedWeights.moe (fused/quantization.py:181-202) and the
  * FusedOps.moe contract (fused/ops.py:108-123) over packed banks.
  * For blocks of up to 32 tokens dflash_moe_workspace_bytes includes partial down
- * rows sized for the current device's CU count (a split-K down GEMM that runs
- * inside the gate/up launch): query it with the call's device current.
+ * rows sized for the current device's CU count (room for the opt-in split-K down GEMM
+ * inside the gate/up launch, dflash_set_split_down): query it with the call's device current.
  */
 int dflash_moe_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, const float* router_logits,
                      const void* router_weight, int64_t top_k, const dflash_w4* gate_up, const dflash_w4* down,
@@ -195,9 +195,10 @@ int dflash_moe_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, co
  * {512, 1024, 2048}, runs the down GEMM in that launch too: each workgroup multiplies
  * the h columns it produced by the matching K-slice of the down bank and writes fp32 partial
  * rows, which the combine adds in a fixed order (deterministic; the fp32 summation order
- * differs from the two-launch form).  dflash_set_split_down(0) turns it off process-wide
- * (for comparisons; on by default); dflash_moe_split_down returns 1 when a call of this
- * shape runs it on the current device, else 0.
+ * differs from the two-launch form).  Opt-in: dflash_set_split_down(1) turns it on
+ * process-wide (off by default: on MI355X the separate down launch measured faster, 57.5
+ * against 64.2 us per T=16 layer); dflash_moe_split_down returns 1 when a call of this shape runs it on
+ * the current device, else 0.
  */
 int dflash_set_split_down(int enable);
 int dflash_moe_split_down(int64_t tokens, int64_t hidden_size, int64_t inter_size, int64_t experts, int64_t top_k,

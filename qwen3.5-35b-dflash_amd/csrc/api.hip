@@ -341,11 +341,11 @@ struct RouteOut {
   int32_t* offsets;
 };
 
-// Split-K down (fused_down in the gate/up launch): a verify block routed in the gate/up
+// Split-K down (SplitDown in the gate/up launch): a verify block routed in the gate/up
 // prologue (one 32-lane row per token), banks of one scale type, H in {512, 1024, 2048}, a
 // workspace with the partial rows for this grid, and unit ranges of at most two passes.
 // Appends the LDS of the down phase to gu's layout.
-std::atomic<int> g_split_down{1};  // dflash_set_split_down (process-wide)
+std::atomic<int> g_split_down{0};  // dflash_set_split_down (process-wide, opt-in)
 
 bool fused_down_fits(const MoeShapes& S, dflash::VerifyParams* gu, const MoeLayout& L, int grid) {
   using namespace dflash;

@@ -790,8 +790,10 @@ __global__ __launch_bounds__(512) void table_prep_kernel(TableParams p) {
 // are unweighted expert outputs and each is scaled first: by wts[t*k+slot]
 // (the routing weight) or gate[t] (the shared-expert sigmoid) -- the same fp32
 // product the expert epilogues otherwise apply.  grid = (T, H / 512),
-// block = 64: a lane owns 8 columns; the rows are read 8 at a time, all loads
-// of a batch in flight together, and added in slot order.
+// block = 64: a lane owns 8 columns; the rows are read kBatch at a time, all
+// loads of a batch in flight together, and added in slot order.  fp32 rows come
+// from verify blocks (top-k + the shared expert: 9 rows at top-8), read in one
+// batch of 16; the prefill's bf16 rows stream in batches of 8.
 template <typename YT>
 __global__ __launch_bounds__(64) void combine_kernel(const YT* __restrict__ y, const int32_t* __restrict__ inv, int T,
                                                      int k, int H, int has_shared, const float* __restrict__ wts,
@@ -801,11 +803,12 @@ __global__ __launch_bounds__(64) void combine_kernel(const YT* __restrict__ y, c
   const int nrows = k + (has_shared ? 1 : 0);
   if (c < H) {
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int s0 = 0; s0 < nrows; s0 += 8) {
-      float4 a[8], b[8];
-      float w[8];
+    constexpr int kBatch = sizeof(YT) == 4 ? 16 : 8;
+    for (int s0 = 0; s0 < nrows; s0 += kBatch) {
+      float4 a[kBatch], b[kBatch];
+      float w[kBatch];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < kBatch; ++i) {
         const int s = min(s0 + i, nrows - 1);
         const int64_t row = s < k ? ld_const(inv, t * k + s) : static_cast<int64_t>(T) * k + t;
         if constexpr (sizeof(YT) == 4) {
@@ -822,7 +825,7 @@ __global__ __launch_bounds__(64) void combine_kernel(const YT* __restrict__ y, c
         w[i] = wts == nullptr ? 1.f : (s < k ? ld_const(wts, t * k + s) : ld_const(gate, t));
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < kBatch; ++i) {
         if (s0 + i < nrows) {
           if (wts != nullptr) {
             a[i].x *= w[i]; a[i].y *= w[i]; a[i].z *= w[i]; a[i].w *= w[i];
@@ -844,47 +847,55 @@ __global__ __launch_bounds__(64) void combine_kernel(const YT* __restrict__ y, c
 
 // Combine of the split-K down: a slot row's y is the sum of its partial rows (row_seg: first
 // partial row and count, consecutive partials part_rps rows apart, in workgroup order), then
-// weighted and added over the slots as combine_kernel does.  grid = (T, H / 512), block = 64.
-__global__ __launch_bounds__(64) void combine_parts_kernel(const float* __restrict__ y, const int2* __restrict__ seg,
-                                                           int rps, const int32_t* __restrict__ inv, int T, int k,
-                                                           int H, int has_shared, const float* __restrict__ wts,
-                                                           const float* __restrict__ gate, uint16_t* __restrict__ out) {
-  const int t = blockIdx.x;
-  const int c = (blockIdx.y * 64 + threadIdx.x) * 8;
+// weighted and added over the slots.  grid = (T, H / 256), block = 512: wave w takes slots
+// w, w + 8, ... and loads up to 8 partials of a slot at once (four columns per lane), so every
+// partial of the block is in flight together; the waves' weighted sums meet in LDS and wave 0
+// adds them in wave order.
+__global__ __launch_bounds__(512) void combine_parts_kernel(const float* __restrict__ y, const int2* __restrict__ seg,
+                                                            int rps, const int32_t* __restrict__ inv, int T, int k,
+                                                            int H, int has_shared, const float* __restrict__ wts,
+                                                            const float* __restrict__ gate, uint16_t* __restrict__ out) {
+  __shared__ float4 wave_sum[8][64];
+  const int t = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int c = blockIdx.y * 256 + lane * 4;
   const int nrows = k + (has_shared ? 1 : 0);
-  if (c >= H) return;
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < nrows; ++s) {
-    const int row = s < k ? ld_const(inv, t * k + s) : T * k + t;
-    const int2 sg = seg[row];
-    const float w = s < k ? ld_const(wts, t * k + s) : ld_const(gate, t);
-    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int j0 = 0; j0 < sg.y; j0 += 4) {
-      float4 a[4], b[4];
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (c < H) {
+    for (int s = wave; s < nrows; s += 8) {
+      const int row = s < k ? ld_const(inv, t * k + s) : T * k + t;
+      const int2 sg = seg[row];
+      const float w = s < k ? ld_const(wts, t * k + s) : ld_const(gate, t);
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int j0 = 0; j0 < sg.y; j0 += 8) {
+        float4 a[8];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {  // four partials in flight together
-        const int64_t r = static_cast<int64_t>(sg.x) + static_cast<int64_t>(rps) * min(j0 + j, sg.y - 1);
-        const float4* src = reinterpret_cast<const float4*>(y + r * H + c);
-        a[j] = src[0];
-        b[j] = src[1];
-      }
+        for (int j = 0; j < 8; ++j) {
+          const int64_t r = static_cast<int64_t>(sg.x) + static_cast<int64_t>(rps) * min(j0 + j, sg.y - 1);
+          a[j] = *reinterpret_cast<const float4*>(y + r * H + c);
+        }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (j0 + j < sg.y) {
-          v[0] += a[j].x; v[1] += a[j].y; v[2] += a[j].z; v[3] += a[j].w;
-          v[4] += b[j].x; v[5] += b[j].y; v[6] += b[j].z; v[7] += b[j].w;
+        for (int j = 0; j < 8; ++j) {
+          if (j0 + j < sg.y) {
+            v.x += a[j].x; v.y += a[j].y; v.z += a[j].z; v.w += a[j].w;
+          }
         }
       }
+      acc.x += v.x * w; acc.y += v.y * w; acc.z += v.z * w; acc.w += v.w * w;
     }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] += v[i] * w;
   }
-  uint4 o;
-  o.x = f32_to_bf16(acc[0]) | (static_cast<uint32_t>(f32_to_bf16(acc[1])) << 16);
-  o.y = f32_to_bf16(acc[2]) | (static_cast<uint32_t>(f32_to_bf16(acc[3])) << 16);
-  o.z = f32_to_bf16(acc[4]) | (static_cast<uint32_t>(f32_to_bf16(acc[5])) << 16);
-  o.w = f32_to_bf16(acc[6]) | (static_cast<uint32_t>(f32_to_bf16(acc[7])) << 16);
-  *reinterpret_cast<uint4*>(out + static_cast<int64_t>(t) * H + c) = o;
+  wave_sum[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0 && c < H) {
+    float4 o = wave_sum[0][lane];
+    for (int i = 1; i < min(8, nrows); ++i) {
+      const float4 u = wave_sum[i][lane];
+      o.x += u.x; o.y += u.y; o.z += u.z; o.w += u.w;
+    }
+    uint2 r;
+    r.x = f32_to_bf16(o.x) | (static_cast<uint32_t>(f32_to_bf16(o.y)) << 16);
+    r.y = f32_to_bf16(o.z) | (static_cast<uint32_t>(f32_to_bf16(o.w)) << 16);
+    *reinterpret_cast<uint2*>(out + static_cast<int64_t>(t) * H + c) = r;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -958,7 +969,7 @@ void launch_combine_bf16(const uint16_t* y, const int32_t* inv, int T, int k, in
 void launch_combine_parts(const float* ypart, const int2* row_seg, int rps, const int32_t* inv, int T, int k, int H,
                           int has_shared, const float* wts, const float* gate, uint16_t* out, hipStream_t stream) {
   if (T <= 0) return;
-  hipLaunchKernelGGL(combine_parts_kernel, dim3(T, (H + 511) / 512), dim3(64), 0, stream, ypart, row_seg, rps, inv, T,
+  hipLaunchKernelGGL(combine_parts_kernel, dim3(T, (H + 255) / 256), dim3(512), 0, stream, ypart, row_seg, rps, inv, T,
                      k, H, has_shared, wts, gate, out);
 }
 

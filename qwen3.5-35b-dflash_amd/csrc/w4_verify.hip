@@ -66,6 +66,10 @@ __device__ __forceinline__ int wave_start(int n, int w) {
 }
 constexpr int kVStrip = 32;      // output columns per down/linear unit (and per combine strip)
 constexpr int kVLds = 158 * 1024;  // one persistent workgroup per CU
+// Rows of the split-K down's h copy hold I + kHPad columns: the pad (3 quarters, zero) lets a
+// chunk of 4 quarters that runs past the row read zero h without a bounds select.
+constexpr int kHPad = 96;
+
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
@@ -124,7 +128,7 @@ __device__ __forceinline__ int2 part_rows(const VerifyParams& vp, int P, int r, 
 // every pass descriptor in pdesc and the token of every slot row in tok;
 // returns the number of passes.  Workgroup 0 writes the routing outputs
 // (ids, weights, perm, inv, offsets) and the work table the down launch reads.
-__device__ int route_block(const VerifyParams& vp, char* lds, int4* pdesc, int* tok) {
+__device__ __forceinline__ int route_block(const VerifyParams& vp, char* lds, int4* pdesc, int* tok) {
   const int T = vp.g.T, E = vp.E, k = vp.g.top_k;
   const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id();
   const int tpad = (T + 3) & ~3;
@@ -361,7 +365,7 @@ __device__ __forceinline__ RowKeys<kPR> route_rows_load(const VerifyParams& vp) 
 }
 
 template <int kPR>
-__device__ int route_rows(const VerifyParams& vp, RowKeys<kPR> keys, char* lds, int4* pdesc, int* tok) {
+__device__ __forceinline__ int route_rows(const VerifyParams& vp, RowKeys<kPR> keys, char* lds, int4* pdesc, int* tok) {
   const int T = vp.g.T, E = vp.E, k = vp.g.top_k;
   const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id(), r = lane & 31;
   const int t0 = 2 * wave + (lane >> 5);  // token of pass 0; pass 1 adds 16
@@ -598,7 +602,7 @@ __device__ __forceinline__ int verify_passes(const VerifyParams& vp, char* lds) 
   if (kMode == kModeGateUp && vp.route == 2) {
     if (vp.fuse_down) {  // h of the workgroup's unit range, zero outside it (the routing's barriers order this)
       uint4* h = reinterpret_cast<uint4*>(lds + vp.lds_h);
-      for (int i = threadIdx.x; i < (2 * 16 * vp.dI * 2) / 16; i += kVThreads) h[i] = make_uint4(0u, 0u, 0u, 0u);
+      for (int i = threadIdx.x; i < (2 * 16 * (vp.dI + kHPad) * 2) / 16; i += kVThreads) h[i] = make_uint4(0u, 0u, 0u, 0u);
     }
     if (vp.E <= 128) {
       const RowKeys<4> keys = route_rows_load<4>(vp);
@@ -746,7 +750,7 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
           if (valid) p.out_bf16[static_cast<int64_t>(hrow) * inter + octet_slot(row0 + lr)] = hb;
           if (valid && vp.fuse_down) {  // pass slot P - P_first of the split-K down (its range spans at most two)
             uint16_t* lh = reinterpret_cast<uint16_t*>(lds + vp.lds_h);
-            lh[((P - P_first) * 16 + 4 * kq + e) * inter + octet_slot(row0 + lr)] = hb;
+            lh[((P - P_first) * 16 + 4 * kq + e) * (inter + kHPad) + octet_slot(row0 + lr)] = hb;
           }
           const float part = row16_sum(valid ? bf16_to_f32(hb) : 0.f);
           if (valid && lr == 0) p.out_part[static_cast<int64_t>(hrow) * (inter >> 4) + strip] = -kDequantOffset * part;
@@ -996,6 +1000,15 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
   }
 }
 
+// Raw bits of one group scale through a buffer resource (byte offsets voff + soff).
+template <typename ScaleT>
+__device__ __forceinline__ uint32_t buf_scale_bits(buf_rsrc r, uint32_t voff, uint32_t soff) {
+  if constexpr (sizeof(ScaleT) == 4)
+    return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(voff), static_cast<int>(soff), 0);
+  else
+    return __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(voff), static_cast<int>(soff), 0);
+}
+
 // Lane quarters <-> words: word D of lane quarter Q becomes word Q of lane quarter D (a 4 x 4
 // transpose of four 32-bit words across the wave's four 16-lane quarters).  permlane32_swap
 // exchanges the upper 32 lanes of its first operand with the lower 32 of its second,
@@ -1014,175 +1027,244 @@ __device__ __forceinline__ void quarter_transpose(uint32_t (&w)[4]) {
 // Split-K down GEMM of a routing gate/up launch (VerifyParams::fuse_down): after its gate/up
 // units, this workgroup holds h for its unit range in LDS -- strips [sa, sb) of at most two
 // passes -- and multiplies each pass's rows by the matching K-slice of the down bank, so the
-// down weights stream inside this launch and no h leaves it.  Work item = one 32-column
-// quarter q of I (two strips) for all of this wave's H / 128 output tiles: per group of 4
-// tiles one 16-byte load per lane (lane quarter Q: tile 4g + Q, its row lane % 16, the
-// quarter's 32 k; contiguous 256 bytes per 16 lanes in the tiled layout), transposed so lane
-// l holds k-octet l / 16 of each tile's row l % 16 -- the B operand of one
-// v_mfma_f32_16x16x32_bf16 per tile -- against the quarter's h fragment; each tile's result is
-// scaled by its group scale and summed over the quarters.  Quarters half inside the range
-// read zero h for the missing strip.  The sums are this workgroup's partial y rows (fp32,
-// unweighted) at 16-row segment b + P; the combine adds every workgroup's partial of a row.
-template <int kN4, typename ScaleT>
-__device__ __forceinline__ void fused_down(const VerifyParams& vp, char* lds, const int total_passes) {
-  // an item is one quarter for one group of 4 tiles; a quarter's kN4 items are consecutive, so
-  // with kQD a multiple of kN4 an item's group is a compile-time index of the unrolled ring
-  constexpr int kQD = kN4 == 4 ? 8 : 6;  // items in flight per wave (one 16-byte load per lane each)
-  static_assert(kQD % kN4 == 0, "ring depth must hold whole quarters");
-  const int strips = vp.g.strips;
-  const int64_t U = static_cast<int64_t>(total_passes) * strips;
-  const int G = static_cast<int>(gridDim.x), b = static_cast<int>(blockIdx.x);
-  const int ub = static_cast<int>(U * b / G), ue = static_cast<int>(U * (b + 1) / G);
-  const int4* lds_pdesc = reinterpret_cast<const int4*>(lds + vp.lds_pdesc);
-  if (ue <= ub) {
-    // An empty range (more workgroups than units) strictly inside pass P's units lies between
-    // the pass's first and last workgroups, whose partial rows the combine adds one by one:
-    // it writes zero rows.  (An empty range at a pass boundary belongs to no pass's run.)
-    const int P = ub / strips;
-    if (ub < U && ub != P * strips) {
-      const int4 d = lds_pdesc[P];
-      const int rows = min(16, d.z - d.w), quads = vp.dH >> 2;
-      float4* o = reinterpret_cast<float4*>(vp.ypart + static_cast<int64_t>(vp.part_rps) * (b + P) * vp.dH);
-      for (int i = threadIdx.x; i < rows * quads; i += kVThreads) o[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    return;
-  }
-  const int I = vp.dI, H = vp.dH, nq = I >> 5, nbq = I >> 7;  // quarters per row, 128-column blocks
-  const int ngd = I / vp.dG, qshift = vp.dG == 256 ? 3 : 2;     // groups per row; quarter -> group
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = lane_id(), lr = lane & 15, kq = lane >> 4;
-  const uint16_t* lh = reinterpret_cast<const uint16_t*>(lds + vp.lds_h);  // [2][16][I]
-  float* lst = reinterpret_cast<float*>(lds + vp.lds_hstart);            // [2][nq][16]
-  const int P0 = ub / strips, np = (ue - 1) / strips - P0 + 1;           // 1 or 2 pass slots
+// down weights stream inside this launch and no h leaves it.  Wave w owns output tiles
+// (16 rows of H) [w H / 128, (w + 1) H / 128).  Work item = four of the wave's tiles and a
+// chunk of four consecutive 32-column quarters of the range: per tile one 16-byte load per
+// lane (lane quarter Q: quarter c + Q, row lane % 16; in the tiled layout a tile's quarters
+// lie 256 bytes apart, so each load is one contiguous kilobyte), transposed so lane l holds
+// k-octet l / 16 of each quarter's row l % 16 -- the B operand of one
+// v_mfma_f32_16x16x32_bf16 per quarter -- against that quarter's h fragment, shared by the
+// four tiles; each quarter's product is scaled by its group scale (a chunk spans at most two
+// groups).  Lanes whose quarter lies past the range load nothing (an offset past the buffer)
+// and meet zero h (h is zero outside the range and in a 3-quarter pad after each row).  After
+// a tile group's last chunk its sums are this workgroup's partial y rows (fp32, unweighted)
+// at 16-row segment b + P; the combine adds every workgroup's partial of a row.  Items are
+// large because the CU's one scalar unit serves all eight waves: per-item uniform work is
+// amortised over 4 KB of weights per wave.  (Issuing the first items as soon as a wave's gate/up
+// k-blocks were done, before the workgroup's partial-sum exchange, measured 7 us slower: the
+// items' registers then overlapped the gate/up state.)
+template <bool kTiled, typename ScaleT>
+struct SplitDown {
+  static constexpr int kQD = 3;  // items in flight per wave (4 16-byte loads per lane each)
+  struct Cursor {
+    int j, g, c, n;  // slot, tile group of the wave, chunk, items left after this one
+  };
+  struct Item {
+    uint4 w[4];
+    uint32_t sa[4], sb[4];  // the chunk's first and last group scale of each tile
+  };
+  const VerifyParams& vp;
+  char* lds;
+  int b, P0, I, H, nq, qshift, hs, nqs, qa0, qb0, qb1, nc0, nc1, nG, tile0, nI;
+  int4 dsc0, dsc1;
+  buf_rsrc wr0, wr1, sr0, sr1;
+  uint32_t wlane, slane, tile_bytes, rowb, sgroup;
+  Cursor ic, cc;
+  Item ring[kQD];
 
-  // quarter ranges and descriptors of the slots (scalars: an array indexed by the runtime
-  // slot would live in scratch memory)
-  auto wave_desc = [&](int P) {
-    const int4 v = lds_pdesc[P];
+  __device__ __forceinline__ SplitDown(const VerifyParams& p, char* l) : vp(p), lds(l) {}
+
+  __device__ __forceinline__ int4 wave_desc(int P) const {
+    const int4 v = reinterpret_cast<const int4*>(lds + vp.lds_pdesc)[P];
     return make_int4(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
                      __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w));
-  };
-  const int sa0 = ub - P0 * strips, sb0 = min(ue, (P0 + 1) * strips) - P0 * strips;
-  const int qa0 = sa0 >> 1, qb0 = (sb0 + 1) >> 1;
-  const int qb1 = np > 1 ? (ue - (P0 + 1) * strips + 1) >> 1 : 0;  // slot 1 starts at quarter 0
-  const int4 dsc0 = wave_desc(P0), dsc1 = wave_desc(P0 + np - 1);
-  const int n0 = qb0 - qa0, nQ = n0 + qb1, nI = nQ * kN4;
-
-  // Loads of item i (clamped: past the end they repeat the last one, never computed).  Tiled:
-  // the quarter of a tile is 256 contiguous bytes (16 rows x 16 bytes); portable: 16 bytes of
-  // each row, rows I / 2 bytes apart (correct, but a row's 128-byte line serves 8 quarters).
-  const bool tiled = vp.g.tiled != 0;
-  const uint32_t tile_bytes = static_cast<uint32_t>(nbq) * 1024u, rowb = static_cast<uint32_t>(I) / 2u;
-  const uint32_t wlane = tiled ? static_cast<uint32_t>(kq) * tile_bytes + static_cast<uint32_t>(lr) * 16u
-                               : static_cast<uint32_t>(16 * kq + lr) * rowb;
-  const int tile0 = wave * 4 * kN4;  // this wave's first output tile (16 rows of H)
-  struct Item {
-    uint4 w;
-    uint32_t s[4];
-  };
-  auto issue = [&](Item& it, int i) {
-    i = max(min(i, nI - 1), 0);
-    const int Q = i / kN4, g = i - Q * kN4;
-    const bool j0 = Q < n0;
-    const int q = j0 ? qa0 + Q : Q - n0;
-    const int4 d = j0 ? dsc0 : dsc1;
-    const bool shared = d.x < 0;
-    const uint8_t* wb = shared ? vp.dw_shared : vp.dw + static_cast<int64_t>(d.x) * vp.dw_stride;
-    const ScaleT* sb = static_cast<const ScaleT*>(shared ? vp.ds_shared : vp.ds) +
-                       (shared ? 0 : static_cast<int64_t>(d.x) * vp.ds_stride);
-    const buf_rsrc wr = make_rsrc(wb, static_cast<uint32_t>(H) * static_cast<uint32_t>(I) / 2);
-    const uint32_t qoff = tiled ? static_cast<uint32_t>(q >> 2) * 1024u + static_cast<uint32_t>(q & 3) * 256u
-                                : static_cast<uint32_t>(q) * 16u;
-    const uint32_t t0 = static_cast<uint32_t>(tile0 + 4 * g);
-    it.w = buf_load16(wr, wlane, (tiled ? t0 * tile_bytes : t0 * 16u * rowb) + qoff);
-    const int gq = q >> qshift;
+  }
+  __device__ __forceinline__ uint32_t wtile(int t) const {
+    return kTiled ? static_cast<uint32_t>(t) * tile_bytes : static_cast<uint32_t>(t) * 16u * rowb;
+  }
+  __device__ __forceinline__ uint32_t stile(int t) const {
+    const int ngd = I / vp.dG;
+    return static_cast<uint32_t>(t * ngd * 16) * static_cast<uint32_t>(sizeof(ScaleT));
+  }
+  // Items in order (slot, tile group, chunk); the issue and compute cursors walk them with no
+  // divisions.  A cursor on the last item stays there (its loads are repeated, never computed).
+  __device__ __forceinline__ void advance(Cursor& k) const {
+    if (k.n == 0) return;
+    --k.n;
+    if (++k.c == (k.j == 0 ? nc0 : nc1)) {
+      k.c = 0;
+      if (++k.g == nG) {
+        k.g = 0;
+        k.j = 1;
+      }
+    }
+  }
+  __device__ __forceinline__ void issue(Item& it) {
+    const bool j0 = ic.j == 0;
+    const int q0 = (j0 ? qa0 : 0) + 4 * ic.c, qb = j0 ? qb0 : qb1;
+    const buf_rsrc wr = j0 ? wr0 : wr1, sr = j0 ? sr0 : sr1;
+    // lanes whose quarter is past the range read nothing (offset past the buffer: no fetch, 0)
+    const uint32_t voff = q0 + (lane_id() >> 4) < qb ? wlane : 0x80000000u;
+    const uint32_t qoff = static_cast<uint32_t>(q0) * (kTiled ? 256u : 16u);
+    const uint32_t ga = static_cast<uint32_t>(q0 >> qshift) * sgroup;
+    const uint32_t gb = static_cast<uint32_t>(min(q0 + 3, nq - 1) >> qshift) * sgroup;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const int64_t tile = tile0 + 4 * g + t;
-      it.s[t] = load_scale_bits(sb + (tiled ? (tile * ngd + gq) * 16 + lr : (tile * 16 + lr) * ngd + gq));
+      const int tile = tile0 + 4 * ic.g + t;
+      it.w[t] = buf_load16(wr, voff, wtile(tile) + qoff);
+      it.sa[t] = buf_scale_bits<ScaleT>(sr, slane, stile(tile) + ga);
+      it.sb[t] = buf_scale_bits<ScaleT>(sr, slane, stile(tile) + gb);
     }
-  };
-  Item ring[kQD];
-#pragma unroll
-  for (int i = 0; i + 1 < kQD; ++i) issue(ring[i], i);
-
-  // every h value of the range is in LDS (the gate/up epilogues); -136 * sum per quarter and row
-  lds_barrier();
-  for (int i = threadIdx.x; i < 2 * nq * 16; i += kVThreads) {
-    const int r = i & 15, q = (i >> 4) % nq, j = i / (16 * nq);
-    const uint4* src = reinterpret_cast<const uint4*>(lh + (j * 16 + r) * I + 32 * q);
-    float sum = 0.f;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint4 v = src[c];
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int h2 = 0; h2 < 4; ++h2) sum += __uint_as_float(w[h2] << 16) + __uint_as_float(w[h2] & 0xFFFF0000u);
-    }
-    lst[(j * nq + q) * 16 + r] = -kDequantOffset * sum;
+    advance(ic);
   }
-  lds_barrier();
 
-  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-  f32x4 tot[kN4][4];
+  // the range [ub, ue) of units, its banks and the cursors; the first items go out
+  __device__ __forceinline__ void start(const int ub, const int ue) {
+    const int strips = vp.g.strips, lane = lane_id();
+    b = static_cast<int>(blockIdx.x);
+    I = vp.dI;
+    H = vp.dH;
+    nq = I >> 5;
+    const int ngd = I / vp.dG;
+    qshift = vp.dG == 256 ? 3 : 2;  // quarter -> group
+    hs = I + kHPad;
+    nqs = nq + 3;  // padded row lengths
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lr = lane & 15, kq = lane >> 4;
+    P0 = ub / strips;
+    const int np = (ue - 1) / strips - P0 + 1;  // 1 or 2 pass slots
+    const int sa0 = ub - P0 * strips, sb0 = min(ue, (P0 + 1) * strips) - P0 * strips;
+    qa0 = __builtin_amdgcn_readfirstlane(sa0 >> 1);
+    qb0 = __builtin_amdgcn_readfirstlane((sb0 + 1) >> 1);
+    qb1 = __builtin_amdgcn_readfirstlane(np > 1 ? (ue - (P0 + 1) * strips + 1) >> 1 : 0);  // from quarter 0
+    dsc0 = wave_desc(P0);
+    dsc1 = wave_desc(P0 + np - 1);
+    nc0 = (qb0 - qa0 + 3) >> 2;
+    nc1 = (qb1 + 3) >> 2;  // chunks of 4 quarters
+    nG = H >> 9;
+    tile0 = wave * 4 * nG;  // tile groups and first tile of the wave
+    nI = nG * (nc0 + nc1);
+    tile_bytes = static_cast<uint32_t>(I >> 7) * 1024u;
+    rowb = static_cast<uint32_t>(I) / 2u;
+    const uint32_t bank_bytes = static_cast<uint32_t>(H) * static_cast<uint32_t>(I) / 2u;
+    auto bank_of = [&](const int4& d) {
+      return d.x < 0 ? vp.dw_shared : vp.dw + static_cast<int64_t>(d.x) * vp.dw_stride;
+    };
+    auto scales_of = [&](const int4& d) {
+      return static_cast<const ScaleT*>(d.x < 0 ? vp.ds_shared : vp.ds) +
+             (d.x < 0 ? 0 : static_cast<int64_t>(d.x) * vp.ds_stride);
+    };
+    wr0 = make_rsrc(bank_of(dsc0), bank_bytes);
+    wr1 = make_rsrc(bank_of(dsc1), bank_bytes);
+    const uint32_t sbytes = static_cast<uint32_t>(H) * static_cast<uint32_t>(ngd) * sizeof(ScaleT);
+    sr0 = make_rsrc(scales_of(dsc0), sbytes);
+    sr1 = make_rsrc(scales_of(dsc1), sbytes);
+    // lane parts of the addresses: weights (lane quarter = quarter of the chunk, lane % 16 =
+    // row) and scales (the lane's row; tiled scales are [tile][group][16], portable [row][group],
+    // both 16 ngd elements per tile)
+    wlane = kTiled ? static_cast<uint32_t>(kq) * 256u + static_cast<uint32_t>(lr) * 16u
+                   : static_cast<uint32_t>(lr) * rowb + static_cast<uint32_t>(kq) * 16u;
+    slane = static_cast<uint32_t>(kTiled ? lr : lr * ngd) * sizeof(ScaleT);
+    sgroup = static_cast<uint32_t>(kTiled ? 16 : 1) * static_cast<uint32_t>(sizeof(ScaleT));
+    ic = Cursor{0, 0, 0, nI - 1};
+    cc = ic;
 #pragma unroll
-  for (int g = 0; g < kN4; ++g)
-#pragma unroll
-    for (int t = 0; t < 4; ++t) tot[g][t] = zero;
-  // this wave's partial y rows of slot j: rows 4 kq + e of its tiles' column lr
-  auto flush = [&](int j) {
-    const int4 d = j == 0 ? dsc0 : dsc1;
-    const int64_t row0 = static_cast<int64_t>(vp.part_rps) * (b + P0 + j);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int r = 4 * kq + e;
-      if (d.w + r < d.z) {
-        float* o = vp.ypart + (row0 + r) * H + tile0 * 16 + lr;
-#pragma unroll
-        for (int g = 0; g < kN4; ++g)
-#pragma unroll
-          for (int t = 0; t < 4; ++t) o[(4 * g + t) * 16] = tot[g][t][e];
-      }
+    for (int i = 0; i + 1 < kQD; ++i) issue(ring[i]);
+  }
+
+  // An empty range (more workgroups than units) strictly inside pass P's units lies between
+  // the pass's first and last workgroups, whose partial rows the combine adds one by one: it
+  // writes zero rows.  (An empty range at a pass boundary belongs to no pass's run.)
+  __device__ __forceinline__ void zero_rows(const int ub, const int64_t U) const {
+    const int strips = vp.g.strips, bb = static_cast<int>(blockIdx.x);
+    const int P = ub / strips;
+    if (ub < U && ub != P * strips) {
+      const int4 d = reinterpret_cast<const int4*>(lds + vp.lds_pdesc)[P];
+      const int rows = min(16, d.z - d.w), quads = vp.dH >> 2;
+      float4* o = reinterpret_cast<float4*>(vp.ypart + static_cast<int64_t>(vp.part_rps) * (bb + P) * vp.dH);
+      for (int i = threadIdx.x; i < rows * quads; i += kVThreads) o[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
+  }
+
+  __device__ __forceinline__ void run(const int total_passes) {
+    const int64_t U = static_cast<int64_t>(total_passes) * vp.g.strips;
+    const int G = static_cast<int>(gridDim.x), bb = static_cast<int>(blockIdx.x);
+    const int ub = static_cast<int>(U * bb / G), ue = static_cast<int>(U * (bb + 1) / G);
+    if (ue <= ub) {
+      zero_rows(ub, U);
+      return;
+    }
+    start(ub, ue);
+    const int lr = lane_id() & 15, kq = lane_id() >> 4;
+    const uint16_t* lh = reinterpret_cast<const uint16_t*>(lds + vp.lds_h);  // [2][16][hs]
+    float* lst = reinterpret_cast<float*>(lds + vp.lds_hstart);            // [2][nqs][16]
+    // every h value of the range is in LDS (the gate/up epilogues); -136 * sum per quarter and row
+    lds_barrier();
+    for (int i = threadIdx.x; i < 2 * nqs * 16; i += kVThreads) {
+      const int r = i & 15, q = (i >> 4) % nqs, j = i / (16 * nqs);
+      const uint4* src = reinterpret_cast<const uint4*>(lh + (j * 16 + r) * hs + 32 * q);
+      float sum = 0.f;
 #pragma unroll
-    for (int g = 0; g < kN4; ++g)
+      for (int c = 0; c < 4; ++c) {
+        const uint4 v = src[c];
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-      for (int t = 0; t < 4; ++t) tot[g][t] = zero;
-  };
-  int cur = 0;
-  uint4 a = make_uint4(0u, 0u, 0u, 0u);
-  f32x4 start = zero;
-  for (int i0 = 0; i0 < nI; i0 += kQD) {
+        for (int h2 = 0; h2 < 4; ++h2) sum += __uint_as_float(w[h2] << 16) + __uint_as_float(w[h2] & 0xFFFF0000u);
+      }
+      lst[(j * nqs + q) * 16 + r] = -kDequantOffset * sum;
+    }
+    lds_barrier();
+
+    const uint16_t* hl = lh + lr * hs + 8 * kq;
+    const float* sl = lst + 4 * kq;
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    f32x4 tot[4] = {zero, zero, zero, zero};
+    for (int i0 = 0; i0 < nI; i0 += kQD) {
 #pragma unroll
-    for (int u = 0; u < kQD; ++u) {
-      const int i = i0 + u;
-      issue(ring[(u + kQD - 1) % kQD], i + kQD - 1);
-      if (i < nI) {
-        const int g = u % kN4;  // == i % kN4: i0 is a multiple of kQD, a multiple of kN4
-        if (g == 0) {           // first item of a quarter: its slot, h fragment and start terms
-          const int Q = i / kN4;
-          const int j = Q < n0 ? 0 : 1;
-          if (j != cur) {
-            flush(cur);
-            cur = j;
+      for (int u = 0; u < kQD; ++u) {
+        issue(ring[(u + kQD - 1) % kQD]);
+        if (i0 + u < nI) {
+          const bool j0 = cc.j == 0;
+          const int q0 = (j0 ? qa0 : 0) + 4 * cc.c;
+          const int ga = q0 >> qshift;
+          // the chunk's h fragments and start terms, shared by the item's four tiles
+          uint4 a[4];
+          f32x4 st[4];
+#pragma unroll
+          for (int dq = 0; dq < 4; ++dq) {
+            a[dq] = *reinterpret_cast<const uint4*>(hl + cc.j * 16 * hs + 32 * (q0 + dq));
+            st[dq] = *reinterpret_cast<const f32x4*>(sl + (cc.j * nqs + q0 + dq) * 16);
           }
-          const int q = j == 0 ? qa0 + Q : Q - n0;
-          a = *reinterpret_cast<const uint4*>(lh + (j * 16 + lr) * I + 32 * q + 8 * kq);
-          start = *reinterpret_cast<const f32x4*>(lst + (j * nq + q) * 16 + 4 * kq);
-        }
-        const Item& it = ring[u];
-        uint32_t w[4] = {it.w.x, it.w.y, it.w.z, it.w.w};
-        quarter_transpose(w);
+          const Item& it = ring[u];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const f32x4 acc = mfma16x16x32(a, dequant8(w[t]), start);
-          tot[g][t] += scale_value<ScaleT>(it.s[t]) * acc;
+          for (int t = 0; t < 4; ++t) {
+            uint32_t w[4] = {it.w[t].x, it.w[t].y, it.w[t].z, it.w[t].w};
+            quarter_transpose(w);
+            const float sa = scale_value<ScaleT>(it.sa[t]), sb = scale_value<ScaleT>(it.sb[t]);
+#pragma unroll
+            for (int dq = 0; dq < 4; ++dq) {
+              const f32x4 acc = mfma16x16x32(a[dq], dequant8(w[dq]), st[dq]);
+              tot[t] += (((q0 + dq) >> qshift) == ga ? sa : sb) * acc;
+            }
+          }
+          if (cc.c == (j0 ? nc0 : nc1) - 1) {  // the tile group's partial y rows: rows 4 kq + e of column lr
+            const int4 d = j0 ? dsc0 : dsc1;
+            const int64_t row0 = static_cast<int64_t>(vp.part_rps) * (b + P0 + cc.j);
+            float* o = vp.ypart + row0 * H + (tile0 + 4 * cc.g) * 16 + lr;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              if (d.w + 4 * kq + e < d.z) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) o[static_cast<int64_t>(4 * kq + e) * H + 16 * t] = tot[t][e];
+              }
+            }
+#pragma unroll
+            for (int t = 0; t < 4; ++t) tot[t] = zero;
+          }
+          advance(cc);
         }
+        __builtin_amdgcn_sched_barrier(0);
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
   }
-  flush(cur);
+};
+
+// gate/up with the split-K down in the same launch
+template <bool kTiled, int kNKB, typename ScaleT>
+__device__ __forceinline__ void gate_up_split_down(const VerifyParams& vp, char* lds, const int total_passes) {
+  verify_gemm<kModeGateUp, kNKB, ScaleT>(vp, lds, total_passes);
+  SplitDown<kTiled, ScaleT> down(vp, lds);
+  down.run(total_passes);
 }
 
 template <int kMode, int kNKB, typename ScaleT>
@@ -1191,9 +1273,13 @@ __global__ __launch_bounds__(512) void w4_verify_kernel(VerifyParams vp) {
   tl_mark(kMode, 0);
   const int total_passes = verify_passes<kMode, kNKB>(vp, lds);
   tl_mark(kMode, 1);
-  verify_gemm<kMode, kNKB, ScaleT>(vp, lds, total_passes);
-  if constexpr (kMode == kModeGateUp) {
-    if (vp.fuse_down) fused_down<kNKB / 4, ScaleT>(vp, lds, total_passes);
+  if (kMode == kModeGateUp && vp.fuse_down) {
+    if constexpr (kMode == kModeGateUp) {
+      if (vp.g.tiled) gate_up_split_down<true, kNKB, ScaleT>(vp, lds, total_passes);
+      else gate_up_split_down<false, kNKB, ScaleT>(vp, lds, total_passes);
+    }
+  } else {
+    verify_gemm<kMode, kNKB, ScaleT>(vp, lds, total_passes);
   }
 #ifdef DFLASH_TIMELINE
   __builtin_amdgcn_s_waitcnt(0);
@@ -1300,13 +1386,15 @@ bool verify_layout(int mode, int T, int K, int N, int E, int k, int has_shared, 
 }
 
 
-int fused_down_lds(int I) { return ((2 * 16 * I * 2 + 15) & ~15) + ((2 * (I / 32) * 16 * 4 + 15) & ~15); }
+int fused_down_lds(int I) {
+  return ((2 * 16 * (I + kHPad) * 2 + 15) & ~15) + ((2 * (I / 32 + 3) * 16 * 4 + 15) & ~15);
+}
 
 bool fused_down_layout(VerifyParams* vp, int I) {
   const int off = (vp->lds_bytes + 15) & ~15;
   if (vp->route != 2 || off + fused_down_lds(I) > kVLds) return false;
   vp->lds_h = off;
-  vp->lds_hstart = off + ((2 * 16 * I * 2 + 15) & ~15);
+  vp->lds_hstart = off + ((2 * 16 * (I + kHPad) * 2 + 15) & ~15);
   vp->lds_bytes = off + fused_down_lds(I);
   return true;
 }

@@ -8,6 +8,7 @@ nonzero status.  There is no CPU or dense fallback (reference policy,
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 from typing import NamedTuple, Optional
 
@@ -365,10 +366,26 @@ def moe_workspace_bytes(tokens: int, hidden: int, inter: int, experts: int, top_
                                                       int(has_shared)))
 
 
+_split_down = False  # the library's process-wide switch, as last set through set_split_down
+
+
 def set_split_down(enable: bool) -> None:
     """Process-wide: run a verify block's down GEMM inside its gate/up launch where it fits
-    (on by default; off runs the separate down launch, for comparisons)."""
+    (opt-in; off, the default, runs the separate down launch)."""
+    global _split_down
     _lib.call("dflash_set_split_down", int(bool(enable)))
+    _split_down = bool(enable)
+
+
+@contextlib.contextmanager
+def split_down(enable: bool):
+    """Sets the split-K down switch for a block of calls and restores the previous setting."""
+    prev = _split_down
+    set_split_down(enable)
+    try:
+        yield
+    finally:
+        set_split_down(prev)
 
 
 def moe_split_down(tokens: int, hidden: int, inter: int, experts: int, top_k: int, group_size: int,

@@ -206,11 +206,15 @@ def test_moe_repeat_calls_are_identical(pkg, device):
 @pytest.fixture
 def two_launches(pkg):
     """The verify block's down GEMM as a launch of its own for one test (the split-K down off)."""
-    pkg.ops.set_split_down(False)
-    try:
+    with pkg.ops.split_down(False):
         yield
-    finally:
-        pkg.ops.set_split_down(True)
+
+
+@pytest.fixture
+def split_on(pkg):
+    """The opt-in split-K down switched on for one test."""
+    with pkg.ops.split_down(True):
+        yield
 
 
 @pytest.mark.parametrize("tokens", [16, 40, 128])
@@ -238,7 +242,7 @@ def test_measure_stage_relaunches_one_kernel(pkg, device, tokens, two_launches):
     assert torch.equal(again, ref)
 
 
-def test_measure_stage_relaunches_the_split_kernel(pkg, device):
+def test_measure_stage_relaunches_the_split_kernel(pkg, device, split_on):
     """T=16: measurement of EXPERTS with the call's router logits relaunches the gate/up launch
     that also runs the split-K down, which rewrites identical bytes."""
     layer = pkg.synthetic.moe_layer(16, seed=6)
@@ -271,7 +275,8 @@ def test_measure_stage_relaunches_the_split_kernel(pkg, device):
     (24, 16, 4, 1024, 512, 128, torch.bfloat16, True, "tiled"),       # full 16-row passes, two shared passes
     (16, 32, 2, 512, 512, 128, torch.bfloat16, False, "tiled"),       # H = 512, no shared expert
 ])
-def test_split_down_layer(pkg, device, tokens, experts, k, hidden, inter, group, scale_dtype, shared, layout):
+def test_split_down_layer(pkg, device, tokens, experts, k, hidden, inter, group, scale_dtype, shared, layout,
+                          split_on):
     """The down GEMM inside the gate/up launch (split over K by each workgroup's strips, partial
     rows added by the combine): on one workspace, a call, a repeat and a smaller block after it
     each route bit-exactly, meet the oracle bar, repeat bit-identically, and agree with the two
@@ -293,11 +298,8 @@ def test_split_down_layer(pkg, device, tokens, experts, k, hidden, inter, group,
         if prev is not None and prev[0] == t:
             assert torch.equal(out, prev[1])
         prev = (t, out.clone())
-        pkg.ops.set_split_down(False)
-        try:
+        with pkg.ops.split_down(False):
             two = pkg.ops.moe_w4a16(x, gu, dn, top_k=k, router_weight=rw, shared=sh)
-        finally:
-            pkg.ops.set_split_down(True)
         ogu, odn, osh = _oracle_banks(layer)
         golden = oracle_moe.moe(layer.hidden, logits.cpu().numpy(), k, ogu, odn, group, shared=osh)
         np.testing.assert_array_equal(r.ids.cpu().numpy(), golden["ids"])
@@ -311,7 +313,7 @@ def test_split_down_layer(pkg, device, tokens, experts, k, hidden, inter, group,
         assert versus["max_rel"] <= 4e-3, versus
 
 
-def test_split_down_refused_shapes_run_two_launches(pkg, device):
+def test_split_down_refused_shapes_run_two_launches(pkg, device, split_on):
     """Shapes outside the split-K down -- unit ranges of more than two passes (T=32 at E=256,
     top-8), H outside {512, 1024, 2048}, blocks routed outside the gate/up launch -- run the
     separate down launch and still meet the oracle bar."""

@@ -241,6 +241,7 @@ def test_split_down_switch_validation(pkg):
     assert lib.dflash_set_split_down(2) == 1
     assert "enable" in lib.dflash_last_error().decode()
     assert lib.dflash_set_split_down(1) == 0
+    assert lib.dflash_set_split_down(0) == 0  # back to the default
     # the query needs no device for shapes it refuses on their arguments
     assert lib.dflash_moe_split_down(0, 2048, 512, 256, 8, 128, 1, 0, 1) == 0
     assert lib.dflash_moe_split_down(16, 1000, 512, 256, 8, 128, 1, 0, 1) == 0

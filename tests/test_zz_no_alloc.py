@@ -2,12 +2,12 @@
 
 Its scratch is a static device array of the library instead of a caller
 workspace; everything else is ``dflash_moe_w4a16``, except that the static
-array has no room for the split-K down's partial rows, so it always runs the
-down GEMM as a launch of its own.  Two calls in a row -- the second with a
+array has no room for the opt-in split-K down's partial rows, so it always runs
+the down GEMM as a launch of its own.  Two calls in a row -- the second with a
 smaller block, so stale scratch from the first is present -- must each give the
 same routing and logits as the workspace entry point on the same inputs, the
-same output bits as that entry point with the split-K down switched off, and an
-output within the oracle bar of its default (split-K) output; a layer that needs
+same output bits as that entry point with the split-K down off (its default),
+and an output within the oracle bar of its split-K output; a layer that needs
 more scratch than the array holds is refused before anything is launched.
 """
 import numpy as np
@@ -33,12 +33,10 @@ def test_noalloc_equals_workspace_entry_on_two_calls(pkg, device, given_logits):
         layer, gu, dn, sh = _layer(pkg, device, tokens, seed)
         x, rw = layer.hidden.to(device), layer.router_weight.to(device)
         kw = {"router_logits": pkg.ops.router_logits(x, rw)} if given_logits else {"router_weight": rw}
-        ref, r_ref, lg_ref = pkg.ops.moe_w4a16(x, gu, dn, top_k=8, shared=sh, return_routing=True, **kw)
-        pkg.ops.set_split_down(False)
-        try:
+        with pkg.ops.split_down(False):
             two = pkg.ops.moe_w4a16(x, gu, dn, top_k=8, shared=sh, **kw)
-        finally:
-            pkg.ops.set_split_down(True)
+        with pkg.ops.split_down(True):
+            ref, r_ref, lg_ref = pkg.ops.moe_w4a16(x, gu, dn, top_k=8, shared=sh, return_routing=True, **kw)
         out, r, lg = pkg.ops.moe_w4a16_noalloc(x, gu, dn, top_k=8, shared=sh, **kw)
         torch.cuda.synchronize()
         assert torch.equal(out, two)
