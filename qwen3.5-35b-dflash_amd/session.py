@@ -134,7 +134,12 @@ class VerifySession:
             self._require_prefill()
             if len(values) > self._block_limit:
                 raise ValueError("proposal block longer than the session's block limit")
-            self._generation += 1          # any older open verification is now stale
+            if self._state.position + len(values) > self.model.capacity:
+                raise ValueError("input would exceed the target context capacity")
+            # the forward writes this block's KV rows where an older open verification keeps its
+            # own (one pending region per session), so from here that verification is stale;
+            # a refused block above leaves it open
+            self._generation += 1
             out = self._run(values)
             predicted = out.top1.tolist()
             expected = (self._next_token, *predicted)

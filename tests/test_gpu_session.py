@@ -89,6 +89,9 @@ def test_verify_transactions(pkg, device):
     v2 = s.verify([7, 8, 9])
     with pytest.raises(RuntimeError, match="stale"):
         v1.commit(0)
+    # a block the context cannot hold is refused before it runs and leaves v2 open
+    with pytest.raises(ValueError, match="capacity"):
+        s.verify([1] * (model.capacity - s.position + 1))
     with pytest.raises(ValueError, match="exceeds"):
         v2.commit(v2.max_accepted_prefix + 1)
     before = s.state
