@@ -20,7 +20,7 @@ PACKAGE_DIR = Path(__file__).resolve().parent
 LIBRARY = PACKAGE_DIR / "libdflash_hip.so"
 TIMELINE_LIBRARY = PACKAGE_DIR / "libdflash_hip_timeline.so"
 SOURCES = ("csrc/api.hip", "csrc/route.hip", "csrc/w4_gemm.hip", "csrc/w4_stream.hip",
-           "csrc/w4_tile.hip", "csrc/w4_verify.hip",
+           "csrc/w4_tile.hip", "csrc/w4_verify.hip", "csrc/w4_small.hip",
            "csrc/repack.hip")
 ARCH = "gfx950"
 FLAGS = (

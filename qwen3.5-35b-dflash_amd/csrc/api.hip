@@ -677,6 +677,9 @@ size_t dflash_qlinear_workspace_bytes(int64_t m, int64_t k, int64_t group_size) 
 
 namespace {
 // Both qlinear entry points: y is bf16 [m][N], or fp32 when y_f32.
+// Widest output (N) that runs the one-round-trip small-block kernel (w4_small.hip).
+constexpr int64_t kSmallLinearMaxN = 10240;
+
 int qlinear_impl(const void* x, int64_t m, const dflash_w4* weight, void* y, bool y_f32, void* workspace,
                  size_t workspace_bytes, void* stream) {
   try {
@@ -693,8 +696,28 @@ int qlinear_impl(const void* x, int64_t m, const dflash_w4* weight, void* y, boo
     if (!workspace || workspace_bytes < need || !aligned16(workspace))
       return fail(DFLASH_ERR_WORKSPACE, "qlinear workspace needs " + std::to_string(need) + " bytes");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    // GEMM kernel: verify (m <= 32), else the streaming kernel (or its per-wave fallback)
     const bool tiled = weight->layout == DFLASH_LAYOUT_TILED;
+    // narrow projections of a short block: the one-round-trip kernel (operands straight into
+    // MFMA fragments, one workgroup per 16 columns); wider ones stage x once per workgroup
+    if (N <= kSmallLinearMaxN &&
+        dflash::small_linear_fits(static_cast<int>(m), static_cast<int>(N), static_cast<int>(K),
+                                  static_cast<int>(weight->group_size))) {
+      dflash::SmallLinearParams sp{};
+      sp.x = static_cast<const uint16_t*>(x);
+      sp.w = static_cast<const uint8_t*>(weight->packed);
+      sp.s = weight->scales;
+      sp.y = y;
+      sp.M = static_cast<int>(m);
+      sp.N = static_cast<int>(N);
+      sp.K = static_cast<int>(K);
+      sp.G = static_cast<int>(weight->group_size);
+      sp.tiled = tiled ? 1 : 0;
+      sp.scale_f32 = weight->scale_dtype == DFLASH_DTYPE_F32 ? 1 : 0;
+      sp.y_f32 = y_f32 ? 1 : 0;
+      dflash::launch_w4_small(sp, st);
+      return launch_status("qlinear");
+    }
+    // GEMM kernel: verify (m <= 32), else the streaming kernel (or its per-wave fallback)
     dflash::VerifyParams vl{};
     // the verify kernel stages at most 16 rows of K = 4096; 17..32 rows run as two launches of it
     const int64_t vrows = K == 4096 && m > 16 && m <= 32 ? 16 : m;

@@ -135,6 +135,21 @@ __device__ __forceinline__ float load_scale<uint16_t>(const uint16_t* p) { retur
 template <>
 __device__ __forceinline__ float load_scale<float>(const float* p) { return *p; }
 
+// Lane quarters <-> words: word D of lane quarter Q becomes word Q of lane quarter D (a 4 x 4
+// transpose of four 32-bit words across the wave's four 16-lane quarters).  permlane32_swap
+// exchanges the upper 32 lanes of its first operand with the lower 32 of its second,
+// permlane16_swap the odd 16-lane rows of the first with the even rows of the second.
+__device__ __forceinline__ void quarter_transpose(uint32_t (&w)[4]) {
+  auto s02 = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+  auto s13 = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+  auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+  auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+  w[0] = s01[0];
+  w[1] = s01[1];
+  w[2] = s23[0];
+  w[3] = s23[1];
+}
+
 // Interleaved position of column c inside its octet (k0 k4 k1 k5 k2 k6 k3 k7).
 __device__ __forceinline__ int octet_slot(int c) { return (c & ~7) | ((c & 3) << 1) | ((c >> 2) & 1); }
 

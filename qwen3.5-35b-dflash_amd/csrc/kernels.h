@@ -256,4 +256,19 @@ constexpr int kTileRowsPerPass = 96;
 bool w4_tile_supports(int mode, int N, int K, int G);
 void launch_w4_tile(int mode, bool fp32_scales, int grid, const W4StreamParams& p, hipStream_t stream);
 
+// Latency-bound W4A16 linear for short blocks and narrow outputs (w4_small.hip): one workgroup
+// per 16 output columns, each wave a run of 128-column k-blocks, every operand loaded straight
+// into MFMA fragments up front and the waves' sums added once through LDS.
+struct SmallLinearParams {
+  const uint16_t* x;       // bf16 [M][K]
+  const uint8_t* w;        // packed int4 [N][K/2], portable or tiled
+  const void* s;           // scales [N][K/G] (tiled: [N/16][K/G][16]), bf16 or fp32
+  void* y;                 // [M][N], bf16 or fp32
+  int M, N, K, G;
+  int tiled, scale_f32, y_f32;
+};
+// M <= 32, K in {512, 1024, 2048, 4096}, G in {128, 256}, N % 16 == 0
+bool small_linear_fits(int M, int N, int K, int G);
+void launch_w4_small(const SmallLinearParams& p, hipStream_t stream);
+
 }  // namespace dflash

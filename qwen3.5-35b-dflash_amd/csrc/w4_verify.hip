@@ -1009,21 +1009,6 @@ __device__ __forceinline__ uint32_t buf_scale_bits(buf_rsrc r, uint32_t voff, ui
     return __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(voff), static_cast<int>(soff), 0);
 }
 
-// Lane quarters <-> words: word D of lane quarter Q becomes word Q of lane quarter D (a 4 x 4
-// transpose of four 32-bit words across the wave's four 16-lane quarters).  permlane32_swap
-// exchanges the upper 32 lanes of its first operand with the lower 32 of its second,
-// permlane16_swap the odd 16-lane rows of the first with the even rows of the second.
-__device__ __forceinline__ void quarter_transpose(uint32_t (&w)[4]) {
-  auto s02 = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
-  auto s13 = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
-  auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
-  auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
-  w[0] = s01[0];
-  w[1] = s01[1];
-  w[2] = s23[0];
-  w[3] = s23[1];
-}
-
 // Split-K down GEMM of a routing gate/up launch (VerifyParams::fuse_down): after its gate/up
 // units, this workgroup holds h for its unit range in LDS -- strips [sa, sb) of at most two
 // passes -- and multiplies each pass's rows by the matching K-slice of the down bank, so the

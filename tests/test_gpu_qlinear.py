@@ -33,6 +33,9 @@ def _case(pkg, m, n, k, group, scale_dtype, seed):
     (24, 128, 2048, 128, torch.float32),
     (16, 512, 2048, 256, torch.float32),    # the reference quantizer's g256 fp32 scales, verify kernel
     (16, 256, 4096, 256, torch.bfloat16),   # g256 at K = 4096
+    (16, 10240, 2048, 128, torch.bfloat16), # the widest output of the small-block kernel
+    (16, 10272, 2048, 128, torch.bfloat16), # one tile pair wider: the staging kernel
+    (32, 96, 512, 256, torch.float32),      # small-block kernel: two row tiles, waves past K
 ])
 def test_qlinear_matches_oracle(pkg, device, m, n, k, group, scale_dtype):
     print(f"qlinear m={m} n={n} k={k} g={group} {scale_dtype}", flush=True)
