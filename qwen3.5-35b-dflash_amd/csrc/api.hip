@@ -677,8 +677,12 @@ size_t dflash_qlinear_workspace_bytes(int64_t m, int64_t k, int64_t group_size) 
 
 namespace {
 // Both qlinear entry points: y is bf16 [m][N], or fp32 when y_f32.
-// Widest output (N) that runs the one-round-trip small-block kernel (w4_small.hip).
-constexpr int64_t kSmallLinearMaxN = 10240;
+// 16-row blocks (w4_small.hip): the one-round-trip kernel up to N = 8192, its streaming form
+// (x kept in registers, persistent workgroups) up to N = 32768, the staging verify kernel
+// above (measured per projection: N = 8192 6.5 against 7.6 us streaming; N = 9216 7.5 against
+// 8.4 one-round-trip; N = 65536 16.1 against 19.1 streaming; LM head 59.7 against 69.1).
+constexpr int64_t kSmallLinearMaxN = 8192;
+constexpr int64_t kSmallStreamMinN = 8193, kSmallStreamMaxN = 32768;
 
 int qlinear_impl(const void* x, int64_t m, const dflash_w4* weight, void* y, bool y_f32, void* workspace,
                  size_t workspace_bytes, void* stream) {
@@ -699,9 +703,13 @@ int qlinear_impl(const void* x, int64_t m, const dflash_w4* weight, void* y, boo
     const bool tiled = weight->layout == DFLASH_LAYOUT_TILED;
     // narrow projections of a short block: the one-round-trip kernel (operands straight into
     // MFMA fragments, one workgroup per 16 columns); wider ones stage x once per workgroup
-    if (N <= kSmallLinearMaxN &&
-        dflash::small_linear_fits(static_cast<int>(m), static_cast<int>(N), static_cast<int>(K),
-                                  static_cast<int>(weight->group_size))) {
+    const bool stream_form =
+        N >= kSmallStreamMinN && N <= kSmallStreamMaxN && dflash::small_linear_stream_fits(static_cast<int>(m), static_cast<int>(N),
+                                                                   static_cast<int>(K),
+                                                                   static_cast<int>(weight->group_size));
+    if (stream_form || (N <= kSmallLinearMaxN &&
+                        dflash::small_linear_fits(static_cast<int>(m), static_cast<int>(N), static_cast<int>(K),
+                                                  static_cast<int>(weight->group_size)))) {
       dflash::SmallLinearParams sp{};
       sp.x = static_cast<const uint16_t*>(x);
       sp.w = static_cast<const uint8_t*>(weight->packed);
@@ -714,7 +722,8 @@ int qlinear_impl(const void* x, int64_t m, const dflash_w4* weight, void* y, boo
       sp.tiled = tiled ? 1 : 0;
       sp.scale_f32 = weight->scale_dtype == DFLASH_DTYPE_F32 ? 1 : 0;
       sp.y_f32 = y_f32 ? 1 : 0;
-      dflash::launch_w4_small(sp, st);
+      if (stream_form) dflash::launch_w4_small_stream(sp, cu_count(), st);
+      else dflash::launch_w4_small(sp, st);
       return launch_status("qlinear");
     }
     // GEMM kernel: verify (m <= 32), else the streaming kernel (or its per-wave fallback)

@@ -270,5 +270,8 @@ struct SmallLinearParams {
 // M <= 32, K in {512, 1024, 2048, 4096}, G in {128, 256}, N % 16 == 0
 bool small_linear_fits(int M, int N, int K, int G);
 void launch_w4_small(const SmallLinearParams& p, hipStream_t stream);
+// its streaming form (persistent workgroups, x in registers): M <= 16
+bool small_linear_stream_fits(int M, int N, int K, int G);
+void launch_w4_small_stream(const SmallLinearParams& p, int grid, hipStream_t stream);
 
 }  // namespace dflash

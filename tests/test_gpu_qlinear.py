@@ -33,9 +33,13 @@ def _case(pkg, m, n, k, group, scale_dtype, seed):
     (24, 128, 2048, 128, torch.float32),
     (16, 512, 2048, 256, torch.float32),    # the reference quantizer's g256 fp32 scales, verify kernel
     (16, 256, 4096, 256, torch.bfloat16),   # g256 at K = 4096
-    (16, 10240, 2048, 128, torch.bfloat16), # the widest output of the small-block kernel
-    (16, 10272, 2048, 128, torch.bfloat16), # one tile pair wider: the staging kernel
+    (16, 8192, 2048, 128, torch.bfloat16),  # the widest output of the small-block kernel
+    (17, 10272, 2048, 128, torch.bfloat16), # 17 rows: the staging kernel
+    (16, 32800, 1024, 128, torch.bfloat16), # past the streaming form: the staging kernel
     (32, 96, 512, 256, torch.float32),      # small-block kernel: two row tiles, waves past K
+    (16, 12384, 2048, 128, torch.bfloat16), # its streaming form (x in registers), 4-tile batches, last one half
+    (5, 16448, 4096, 256, torch.float32),   # streaming form at K = 4096: 2-tile batches
+    (9, 12320, 1024, 128, torch.bfloat16),  # streaming form, 8-tile batches, last one a quarter
 ])
 def test_qlinear_matches_oracle(pkg, device, m, n, k, group, scale_dtype):
     print(f"qlinear m={m} n={n} k={k} g={group} {scale_dtype}", flush=True)
