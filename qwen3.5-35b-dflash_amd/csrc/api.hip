@@ -324,6 +324,9 @@ bool verify_fits(const MoeShapes& S, bool route, dflash::VerifyParams* gu, dflas
   if (S.T > kVerifyMaxTokens && moe_tile_path(S)) return false;
   const int T = static_cast<int>(S.T), H = static_cast<int>(S.H), I = static_cast<int>(S.I);
   const int E = static_cast<int>(S.E), k = static_cast<int>(S.k), sh = S.shared ? 1 : 0;
+  // the kernels split units (passes x strips) over the grid in 32-bit arithmetic
+  const int64_t units = verify_pass_cap(S.T, S.E, S.k, S.shared) * std::max(S.I / 16, S.H / 32);
+  if (units * cu_count() >= (int64_t{1} << 32)) return false;
   *gu = VerifyParams{};
   *dn = VerifyParams{};
   return verify_layout(kModeGateUp, T, H, 2 * I, E, k, sh, route ? 1 : 0, gu) &&

@@ -652,7 +652,10 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
 
   const int strips = p.strips;
   const int rank = static_cast<int>(blockIdx.x), ranks = static_cast<int>(gridDim.x);
-  const int64_t total_units = static_cast<int64_t>(total_passes) * strips;
+  // 32-bit unit arithmetic: every wave of the workgroup runs this prologue on the CU's one
+  // scalar unit, where a 64-bit division costs ~130 instructions (the host admits only shapes
+  // with passes x strips x grid < 2^32)
+  const uint32_t total_units = static_cast<uint32_t>(total_passes) * static_cast<uint32_t>(strips);
   // linear mode: workgroup b runs units b, b + G, b + 2G, ... (G = grid), so at any moment the
   // workgroups stream one contiguous window of the weights (contiguous ranges per workgroup
   // leave ~2048 streams a fixed stride apart, which streamed up to 10% slower); its virtual
@@ -660,12 +663,13 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
   int ub, ue;
   if (kMode == kModeLinear) {
     const int G = static_cast<int>(gridDim.x), b = static_cast<int>(blockIdx.x);
-    const int q = static_cast<int>(total_units / G), r = static_cast<int>(total_units % G);
+    const int q = static_cast<int>(total_units / static_cast<uint32_t>(G));
+    const int r = static_cast<int>(total_units - static_cast<uint32_t>(q) * static_cast<uint32_t>(G));
     ub = b * q + min(b, r);
     ue = ub + q + (b < r ? 1 : 0);
   } else {
-    ub = static_cast<int>(total_units * rank / ranks);
-    ue = static_cast<int>(total_units * (rank + 1) / ranks);
+    ub = static_cast<int>(total_units * static_cast<uint32_t>(rank) / static_cast<uint32_t>(ranks));
+    ue = static_cast<int>(total_units * static_cast<uint32_t>(rank + 1) / static_cast<uint32_t>(ranks));
   }
   // the unit that virtual unit v of this workgroup's range stands for
   auto unit_of = [&](int v) {
@@ -1150,10 +1154,10 @@ struct SplitDown {
   // An empty range (more workgroups than units) strictly inside pass P's units lies between
   // the pass's first and last workgroups, whose partial rows the combine adds one by one: it
   // writes zero rows.  (An empty range at a pass boundary belongs to no pass's run.)
-  __device__ __forceinline__ void zero_rows(const int ub, const int64_t U) const {
+  __device__ __forceinline__ void zero_rows(const int ub, const uint32_t U) const {
     const int strips = vp.g.strips, bb = static_cast<int>(blockIdx.x);
     const int P = ub / strips;
-    if (ub < U && ub != P * strips) {
+    if (static_cast<uint32_t>(ub) < U && ub != P * strips) {
       const int4 d = reinterpret_cast<const int4*>(lds + vp.lds_pdesc)[P];
       const int rows = min(16, d.z - d.w), quads = vp.dH >> 2;
       float4* o = reinterpret_cast<float4*>(vp.ypart + static_cast<int64_t>(vp.part_rps) * (bb + P) * vp.dH);
@@ -1162,8 +1166,8 @@ struct SplitDown {
   }
 
   __device__ __forceinline__ void run(const int total_passes) {
-    const int64_t U = static_cast<int64_t>(total_passes) * vp.g.strips;
-    const int G = static_cast<int>(gridDim.x), bb = static_cast<int>(blockIdx.x);
+    const uint32_t U = static_cast<uint32_t>(total_passes) * static_cast<uint32_t>(vp.g.strips);  // U G < 2^32
+    const uint32_t G = gridDim.x, bb = blockIdx.x;
     const int ub = static_cast<int>(U * bb / G), ue = static_cast<int>(U * (bb + 1) / G);
     if (ue <= ub) {
       zero_rows(ub, U);
