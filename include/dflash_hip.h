@@ -201,6 +201,16 @@ int dflash_moe_w4a16(const void* hidden, int64_t tokens, int64_t hidden_size, co
  * the current device, else 0.
  */
 int dflash_set_split_down(int enable);
+
+/*
+ * Tail split of the long-prefill tile kernels (no counterpart in the reference; a test and
+ * measurement override).  The tiles left over after the grid's last full round run in pieces:
+ * by default 4 per tile when they fill at most a quarter of the grid, 2 when at most half,
+ * else whole.  Pieces change only the fp32 summation order of h's -136*sum partials.
+ * dflash_set_tile_pieces(1, 2 or 4) forces that many pieces, 0 restores the default.
+ * Process-wide.
+ */
+int dflash_set_tile_pieces(int pieces);
 int dflash_moe_split_down(int64_t tokens, int64_t hidden_size, int64_t inter_size, int64_t experts, int64_t top_k,
                           int64_t group_size, int has_shared, int32_t scale_dtype, int32_t layout);
 

@@ -69,6 +69,7 @@ SIGNATURES = {
     "dflash_moe_w4a16_noalloc": (ctypes.c_int, [_P, _I64, _I64, _P, _P, _I64, _W4P, _W4P, _W4P, _W4P, _P, _P, _P, _P,
                                                 _P, _P, _P, _P, _P]),
     "dflash_set_split_down": (ctypes.c_int, [ctypes.c_int]),
+    "dflash_set_tile_pieces": (ctypes.c_int, [ctypes.c_int]),
     "dflash_moe_split_down": (ctypes.c_int, [_I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_int, ctypes.c_int32,
                                              ctypes.c_int32]),
     "dflash_set_measure_stage": (ctypes.c_int, [ctypes.c_int]),

@@ -286,11 +286,16 @@ bool stage_on(int stage) {
 // fallback (w4_gemm: K outside {512, 1024, 2048} or group 256).
 enum class GemmPath { kTile, kStream };
 
+// dflash_set_tile_pieces (process-wide): 0 lets the tile kernels split their last round by the
+// grid, 1, 2 or 4 force that many pieces per remaining tile.
+std::atomic<int> g_tile_pieces{0};
+
 void launch_w4(int mode, bool fp32_scales, int mt, int max_slots, GemmPath path, dflash::W4StreamParams& p,
                hipStream_t stream) {
   using namespace dflash;
   if (path == GemmPath::kTile) {
     p.strips = mode == kModeGateUp ? p.N / 2 / 256 : p.N / 512;  // column tiles per pass
+    p.tile_pieces = g_tile_pieces.load(std::memory_order_acquire);
     launch_w4_tile(mode, fp32_scales, cu_count(), p, stream);
     return;
   }
@@ -1030,6 +1035,13 @@ int dflash_moe_w4a16_noalloc(const void* hidden, int64_t tokens, int64_t hidden_
   return moe_w4a16_body(hidden, tokens, hidden_size, router_logits, router_weight, top_k, gate_up, down,
                         shared_gate_up, shared_down, shared_gate_weight, out, logits_out, topk_ids, topk_weights,
                         perm, inv_perm, expert_offsets, nullptr, 0, true, stream);
+}
+
+int dflash_set_tile_pieces(int pieces) {
+  if (pieces != 0 && pieces != 1 && pieces != 2 && pieces != 4)
+    return fail(DFLASH_ERR_INVALID_ARGUMENT, "pieces must be 0, 1, 2 or 4");
+  g_tile_pieces.store(pieces, std::memory_order_release);
+  return DFLASH_OK;
 }
 
 int dflash_set_split_down(int enable) {

@@ -138,6 +138,7 @@ struct W4StreamParams {
   const float* shared_gate;// kModeDown: sigmoid gate [T]
   int M;                   // kModeLinear rows
   int tiled;               // banks in the tiled layout (DFLASH_LAYOUT_TILED), else portable
+  int tile_pieces;         // tile kernels: pieces per tile past the grid's last full round (0: by the grid)
 };
 
 // Portable -> tiled repack of a packed bank and its scales (repack.hip).

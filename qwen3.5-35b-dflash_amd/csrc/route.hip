@@ -498,11 +498,17 @@ __global__ void route_zero_kernel(uint32_t* __restrict__ words, int64_t n) {
     words[i] = 0u;
 }
 
-// grid = ceil(T/4), block = 256: one wave per token.
+// grid = ceil(T/4) + prep blocks, block = 256: one wave per token, then the prep blocks, each
+// taking rows b, b + B, ... (B = prep blocks, at most kMaxPrepBlocks, so the grid's work-item
+// count stays far below 2^32 at any T the routing accepts).
 __global__ __launch_bounds__(256) void route_topk_kernel(RouteParams p) {
   const int topk_blocks = (p.T + 3) >> 2;
-  if (static_cast<int>(blockIdx.x) >= topk_blocks) {  // prep blocks: one row each
-    prep_row(p.prep_x, p.prep_H, blockIdx.x - topk_blocks, p.prep_x_il, p.prep_xneg, p.prep_gate_w, p.prep_gate_out);
+  if (static_cast<int>(blockIdx.x) >= topk_blocks) {
+    const int b = static_cast<int>(blockIdx.x) - topk_blocks, nb = static_cast<int>(gridDim.x) - topk_blocks;
+    for (int row = b; row < p.prep_rows; row += nb) {
+      if (row != b) __syncthreads();  // the previous row's gate partials are read
+      prep_row(p.prep_x, p.prep_H, row, p.prep_x_il, p.prep_xneg, p.prep_gate_w, p.prep_gate_out);
+    }
     return;
   }
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -928,6 +934,9 @@ int64_t route_zero_words(int T, int E) {
   return ((E + 3) & ~3) + static_cast<int64_t>(E) * route_slot_pitch(T) / 4;
 }
 
+// Prep blocks of a route_topk launch: one per row up to this many (T = 2048 prefill: one each).
+constexpr int kMaxPrepBlocks = 16384;
+
 void launch_route(const RouteParams& p, bool zeroed, hipStream_t stream) {
   if (route_small_fits(p.T, p.E, p.k)) {
     hipLaunchKernelGGL(route_small_kernel, dim3(1), dim3(1024), 0, stream, p);
@@ -939,7 +948,9 @@ void launch_route(const RouteParams& p, bool zeroed, hipStream_t stream) {
     hipLaunchKernelGGL(route_zero_kernel, dim3(blocks), dim3(256), 0, stream,
                        reinterpret_cast<uint32_t*>(p.counts), words);
   }
-  if (p.T > 0) hipLaunchKernelGGL(route_topk_kernel, dim3((p.T + 3) / 4 + p.prep_rows), dim3(256), 0, stream, p);
+  if (p.T > 0)
+    hipLaunchKernelGGL(route_topk_kernel, dim3((p.T + 3) / 4 + std::min(p.prep_rows, kMaxPrepBlocks)), dim3(256), 0,
+                       stream, p);
   if (static_cast<int64_t>(p.T) * p.k <= kPermuteCountPairs && reinterpret_cast<uintptr_t>(p.ids) % 16 == 0) {
     hipLaunchKernelGGL(route_permute_kernel<true>, dim3((p.E + 3) / 4), dim3(256), 0, stream, p);
     return;

@@ -423,8 +423,9 @@ __global__ __launch_bounds__(512) void w4_tile_kernel(W4StreamParams p) {
   // quarter of the grid, 2 when at most half): work items [0, full) are whole tiles, then
   // `pieces` per remaining tile (piece q: half-width column piece q & 1, row half q >> 1 when
   // there are 4).  A row half with no rows (one-subtile pass) is an empty item.
+  // (p.tile_pieces, when set, forces 1, 2 or 4: a test and measurement override)
   const int grid = static_cast<int>(gridDim.x), rest = total % grid;
-  const int pieces = 4 * rest <= grid ? 4 : 2 * rest <= grid ? 2 : 1;
+  const int pieces = p.tile_pieces ? p.tile_pieces : 4 * rest <= grid ? 4 : 2 * rest <= grid ? 2 : 1;
   const int split = pieces > 1 ? rest : 0;
   const int full = total - split, items = full + pieces * split;
   // Each workgroup takes its first item by index, then asks a queue for more; every

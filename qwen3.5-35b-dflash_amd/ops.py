@@ -388,6 +388,17 @@ def split_down(enable: bool):
         set_split_down(prev)
 
 
+@contextlib.contextmanager
+def tile_pieces(pieces: int):
+    """Forces the prefill tile kernels' tail split (1, 2 or 4 pieces) for a block of calls,
+    then restores the grid-chosen default."""
+    _lib.call("dflash_set_tile_pieces", int(pieces))
+    try:
+        yield
+    finally:
+        _lib.call("dflash_set_tile_pieces", 0)
+
+
 def moe_split_down(tokens: int, hidden: int, inter: int, experts: int, top_k: int, group_size: int,
                    has_shared: bool, scale_dtype: torch.dtype = torch.bfloat16, layout: str = "tiled") -> bool:
     """Whether a ``moe_w4a16`` call of this shape runs the split-K down on the current device."""

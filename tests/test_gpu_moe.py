@@ -92,6 +92,75 @@ def test_moe_prefill_t2048(pkg, device):
     assert torch.equal(out_p, out_t)
 
 
+def _tile_pass_subtiles(offsets, tokens, rows=96):
+    """16-row subtiles of every pass of the tile kernels, in their queue order: the shared
+    expert's passes, then the routed passes by descending subtile count."""
+    routed = []
+    for c in (offsets[1:] - offsets[:-1]).tolist():
+        routed += [min(rows, c - i) // 16 + (min(rows, c - i) % 16 > 0) for i in range(0, c, rows)]
+    shared = [min(rows, tokens - i) // 16 + (min(rows, tokens - i) % 16 > 0) for i in range(0, tokens, rows)]
+    return shared + sorted(routed, reverse=True)
+
+
+@pytest.mark.timeout(300)
+def test_prefill_tail_pieces(pkg, device):
+    """Each tail split of the tile kernels (whole tiles, 2 half-width pieces, 4 pieces with row
+    halves -- uneven halves of odd-subtile passes included) against the fp64 golden, and the
+    three against each other: routing identical, outputs within the fp32 summation order of h's
+    -136*sum partials."""
+    layer = pkg.synthetic.moe_layer(2304, seed=21)
+    gu, dn, sh = _to(pkg, layer, device)
+    gu, dn, sh = gu.tiled(), dn.tiled(), sh.tiled()
+    x, rw = layer.hidden.to(device), layer.router_weight.to(device)
+    outs = {}
+    for pieces in (1, 2, 4):
+        print(f"prefill T=2304 tail pieces={pieces}", flush=True)
+        with pkg.ops.tile_pieces(pieces):
+            out, r, logits = pkg.ops.moe_w4a16(x, gu, dn, top_k=8, router_weight=rw, shared=sh, return_routing=True)
+        outs[pieces] = (out.cpu(), r.ids.cpu(), r.offsets.cpu())
+    offsets = outs[1][2]
+    grid = torch.cuda.get_device_properties(device).multi_processor_count
+    subtiles = _tile_pass_subtiles(offsets, 2304)
+    for name, ntiles in (("gate/up", 2), ("down", 4)):
+        rest = len(subtiles) * ntiles % grid
+        tail = subtiles[len(subtiles) - (rest + ntiles - 1) // ntiles:] if rest else []
+        print(f"  {name}: {len(subtiles)} passes, {rest} tail tiles of {grid}, their passes' subtiles "
+              f"{sorted(set(tail))}", flush=True)
+        assert rest, "every tile in full rounds: no tail to split"
+        assert any(n % 2 for n in tail), "no odd-subtile pass in the tail: the uneven row halves go untested"
+    ogu, odn, osh = _oracle_banks(layer)
+    golden = oracle_moe.moe(layer.hidden, logits.cpu().numpy(), 8, ogu, odn, 128, shared=osh)
+    for pieces, (out, ids, off) in outs.items():
+        assert torch.equal(ids, outs[1][1]) and torch.equal(off, offsets)
+        report = metrics.compare(out, golden["out_f32"])
+        versus = metrics.compare(out, outs[1][0].float().numpy())
+        print(f"  pieces={pieces} {report} vs whole tiles max_rel={versus['max_rel']:.2e}", flush=True)
+        assert report["max_rel"] <= TOL and report["cosine"] > 0.9999, report
+        assert versus["max_rel"] <= 4e-3, versus
+
+
+@pytest.mark.timeout(300)
+def test_moe_prefill_past_the_prep_block_cap(pkg, device):
+    """T=16400 (above the 16384 prep blocks of a route_topk launch, so 16 prep blocks convert a
+    second row): every token's routing and output equal those of the same tokens run as two
+    halves of 8200 (rows are independent; outputs within the fp32 order of the tail pieces)."""
+    print("moe T=16400 E=64 k=4: whole vs halves", flush=True)
+    layer = pkg.synthetic.moe_layer(16400, experts=64, seed=12)
+    gu, dn, sh = _to(pkg, layer, device)
+    gu, dn, sh = gu.tiled(), dn.tiled(), sh.tiled()
+    x, rw = layer.hidden.to(device), layer.router_weight.to(device)
+    whole, r, _ = pkg.ops.moe_w4a16(x, gu, dn, top_k=4, router_weight=rw, shared=sh, return_routing=True)
+    parts = [pkg.ops.moe_w4a16(x[a:a + 8200].contiguous(), gu, dn, top_k=4, router_weight=rw, shared=sh,
+                               return_routing=True) for a in (0, 8200)]
+    assert torch.equal(r.ids, torch.cat([q[1].ids for q in parts]))
+    halves = torch.cat([q[0] for q in parts])
+    report = metrics.compare(whole.float().cpu(), halves.float().cpu().numpy())
+    print(f"  whole vs halves {report}", flush=True)
+    assert report["max_rel"] <= 4e-3 and report["cosine"] > 0.99999, report
+    tail = metrics.compare(whole[16384:].float().cpu(), halves[16384:].float().cpu().numpy())
+    assert tail["max_rel"] <= 4e-3, tail
+
+
 def _logit_error_bound(hidden, router_weight):
     """Worst-case error of an fp32 dot product of bf16 vectors (products exact in fp32, n-term
     recursive sum): |err| <= n * 2^-24 / (1 - n * 2^-24) * sum|x_i w_i|, per (token, expert)."""

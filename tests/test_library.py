@@ -236,6 +236,15 @@ def test_measure_stage_validation(pkg):
     assert lib.dflash_set_measure_stage(0) == 0
 
 
+def test_tile_pieces_switch_validation(pkg):
+    lib = pkg._lib.load()
+    for bad in (-1, 3, 5, 8):
+        assert lib.dflash_set_tile_pieces(bad) == 1
+        assert "pieces" in lib.dflash_last_error().decode()
+    for good in (1, 2, 4, 0):
+        assert lib.dflash_set_tile_pieces(good) == 0
+
+
 def test_split_down_switch_validation(pkg):
     lib = pkg._lib.load()
     assert lib.dflash_set_split_down(2) == 1
