@@ -5,9 +5,9 @@
 // segment or of the shared expert) times one strip of 2 x 16 weight rows over
 // the full reduction length K.  Units form one list (pass-major); each
 // workgroup takes an equal contiguous range of it, and inside the workgroup the
-// range's k-blocks (128 columns of K) are split evenly over the 8 waves at
-// multiples of 4 k-blocks, so every wave streams the same number of weight
-// bytes whatever the unit count.  A unit whose k-blocks fall to several waves
+// range's k-blocks (128 columns of K) are split over the 8 waves in fixed shares
+// (wave_start: 4 parts for each of waves 0-3 to 3 for each of waves 4-7, which
+// share their SIMDs with the older waves).  A unit whose k-blocks fall to several waves
 // is finished by the wave holding its last k-block, after the others left their
 // partial sums in LDS (summed in wave order: the result does not depend on
 // timing).
@@ -35,7 +35,12 @@
 //             per workgroup, an L2 write-back on every XCD, which measured
 //             slower than one more launch.)
 //   linear  : the raw x rows of a plain qlinear, converted while staged (one
-//             launch per qlinear); one pass per 16 rows.
+//             launch per qlinear); one pass per 16 rows.  Used for outputs wider
+//             than the small-block kernels take (the LM head) and for 17-32 rows
+//             above N = 8192.
+//   gate/up with SplitDown (opt-in, VerifyParams::fuse_down): the down GEMM of
+//             the workgroup's own h columns runs in the same launch, split over K;
+//             fp32 partial rows for combine_parts_kernel.
 //
 // Semantics per mode (reference citations):
 //   kModeLinear : y = x . dequant(W)^T, bf16 out                 (fused/quantization.py:154-165)
