@@ -52,6 +52,27 @@ def test_qlinear_matches_oracle(pkg, device, m, n, k, group, scale_dtype):
     assert report["cosine"] > 0.9999, report
 
 
+@pytest.mark.parametrize("m,n,k,group,scale_dtype", [
+    (16, 256, 2048, 128, torch.bfloat16),   # a packed router's logits: small-block kernel
+    (3, 12384, 1024, 256, torch.float32),   # streaming form
+    (16, 40960, 2048, 128, torch.bfloat16), # staging verify kernel
+    (20, 2048, 512, 128, torch.bfloat16),   # small-block kernel, two row tiles
+])
+def test_qlinear_fp32_output(pkg, device, m, n, k, group, scale_dtype):
+    """The unrounded fp32 output (dflash_qlinear_w4a16_f32): within fp32 summation-order error of
+    the fp64 golden, and its bf16 rounding equal to the bf16 entry's output."""
+    print(f"qlinear fp32 out m={m} n={n} k={k} g={group} {scale_dtype}", flush=True)
+    x, weight = _case(pkg, m, n, k, group, scale_dtype, seed=m + n + 1)
+    xd, wd = x.to(device), weight.to(device)
+    y32 = pkg.ops.qlinear(xd, wd, out_dtype=torch.float32)
+    y16 = pkg.ops.qlinear(xd, wd)
+    assert y32.dtype == torch.float32 and tuple(y32.shape) == (m, n)
+    golden = w4.qlinear(x, weight.packed.numpy(), weight.scales, group)
+    report = metrics.compare(y32.cpu(), golden)
+    assert report["max_rel"] <= 5e-5, report  # fp32 sums of -136-offset products, no bf16 rounding
+    assert torch.equal(y32.to(torch.bfloat16), y16)
+
+
 # The target model's quantized projections at a 16-token verify block (graph/quant_plan.py:25-32):
 # GDN in_proj_qkv / in_proj_z / in_proj_a|b / out_proj (32 value heads x 128, 16 key heads x 128,
 # fused/ops.py:354-360), attention q (gated) / k|v / o (head_dim 256), shared expert gate|up / down.

@@ -37,22 +37,25 @@ def test_to_tiled_matches_oracle(pkg, device, experts, rows, cols, group, scale_
     np.testing.assert_array_equal(got_s, ref_s)
 
 
-@pytest.mark.parametrize("m,n,k,scale_dtype", [
-    (16, 512, 2048, torch.bfloat16),   # verify kernel (linear mode)
-    (5, 96, 1024, torch.float32),
-    (64, 256, 2048, torch.bfloat16),   # streaming kernel
-    (48, 64, 512, torch.float32),
+@pytest.mark.parametrize("m,n,k,group,scale_dtype", [
+    (16, 512, 2048, 128, torch.bfloat16),   # small-block kernel
+    (5, 96, 1024, 128, torch.float32),
+    (32, 160, 4096, 256, torch.float32),    # small-block kernel: two row tiles, 4 k-blocks a wave, g256
+    (16, 12384, 2048, 256, torch.float32),  # its streaming form, g256 fp32 scales
+    (7, 40960, 2048, 128, torch.bfloat16),  # staging verify kernel (linear mode)
+    (64, 256, 2048, 128, torch.bfloat16),   # streaming kernel
+    (48, 64, 512, 128, torch.float32),
 ])
-def test_qlinear_tiled_equals_portable(pkg, device, m, n, k, scale_dtype):
-    print(f"qlinear tiled m={m} n={n} k={k} {scale_dtype}", flush=True)
+def test_qlinear_tiled_equals_portable(pkg, device, m, n, k, group, scale_dtype):
+    print(f"qlinear tiled m={m} n={n} k={k} g={group} {scale_dtype}", flush=True)
     gen = torch.Generator().manual_seed(m + n + k)
     x = torch.randn((m, k), generator=gen).to(torch.bfloat16)
-    w = pkg.synthetic.int4_weight(gen, (n, k), 128, scale_dtype)
+    w = pkg.synthetic.int4_weight(gen, (n, k), group, scale_dtype)
     wd = w.to(device)
     y_p = pkg.ops.qlinear(x.to(device), wd)
     y_t = pkg.ops.qlinear(x.to(device), wd.tiled())
     assert torch.equal(y_p, y_t)
-    report = metrics.compare(y_t.cpu(), w4.qlinear(x, w.packed.numpy(), w.scales, 128))
+    report = metrics.compare(y_t.cpu(), w4.qlinear(x, w.packed.numpy(), w.scales, group))
     assert report["max_rel"] <= TOL, report
 
 
