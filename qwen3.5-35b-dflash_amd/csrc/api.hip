@@ -1072,9 +1072,12 @@ int dflash_moe_split_down(int64_t tokens, int64_t hidden_size, int64_t inter_siz
 
 #ifdef DFLASH_TIMELINE
 // Profiling build only (timeline.py; not in the product ABI): which 0 = verify launches
-// (2 x 1024 x 16 ticks), 1 = tile launches (2 x 1024 x 8 x 3).
+// (2 x 1024 x 16 ticks), 1 = tile launches (2 x 1024 x 8 x 3), 2 = the tile launches' per-wave
+// cycles (2 x 1024 x 8 x 8 x 6).
 int dflash_timeline_read(int which, void* host, size_t bytes) {
-  return which == 0 ? dflash::timeline_verify_read(host, bytes) : dflash::timeline_tile_read(host, bytes);
+  return which == 0 ? dflash::timeline_verify_read(host, bytes)
+       : which == 1 ? dflash::timeline_tile_read(host, bytes)
+                    : dflash::timeline_tile_cycles_read(host, bytes);
 }
 int dflash_timeline_clear(void) { return dflash::timeline_verify_clear() | dflash::timeline_tile_clear(); }
 #endif

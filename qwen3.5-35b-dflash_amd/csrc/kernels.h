@@ -233,6 +233,7 @@ struct VerifyParams {
 int timeline_verify_read(void* host, size_t bytes);
 int timeline_verify_clear();
 int timeline_tile_read(void* host, size_t bytes);
+int timeline_tile_cycles_read(void* host, size_t bytes);
 int timeline_tile_clear();
 #endif
 // LDS bytes and layout of one verify launch; false when it does not fit (the

@@ -51,8 +51,14 @@ constexpr int kTileM = 96;                  // rows per pass (6 subtiles of 16)
 // at the tile's start and end and the tile's rows | pass << 16 | (order + 1) << 40 | half << 56
 // (1 for a piece of a split tile; rows are the whole pass's).
 #ifdef DFLASH_TIMELINE
-constexpr int kTlWorkgroups = 1024, kTlTiles = 8;
+constexpr int kTlWorkgroups = 1024, kTlTiles = 8, kWavesTl = 8;
 __device__ unsigned long long g_timeline_tile[2 * kTlWorkgroups * kTlTiles * 3];
+// Per launch mode, workgroup, its first 8 items and wave, in s_memtime cycles: the item's
+// set-up in three parts (pass entry loaded; the barrier, which also waits for the row id
+// loads and the previous item's stores; the first stage loads and weight reads), the k-loop,
+// the epilogue (to the issue of its last store), and 1 (a written slot).
+constexpr int kTlCycleFields = 6;
+__device__ unsigned long long g_timeline_tile_cycles[2 * kTlWorkgroups * kTlTiles * kWavesTl * kTlCycleFields];
 #endif
 constexpr int kMaxSub = kTileM / 16;
 constexpr int kWaves = 8;
@@ -87,6 +93,10 @@ struct TileCtx {
   uint32_t noff;            // byte offset of the -136*sum terms of row 64 * wave + lane
   buf_rsrc grs;             // down: the pass rows' routing weights (or shared-expert gates)
   uint32_t goff;            // byte offset of the weight of row 64 * wave + lane
+#ifdef DFLASH_TIMELINE
+  unsigned long long t_start, t_ctx, t_sync;  // s_memtime at the start of the work item, its ids loaded, after its barrier
+  unsigned long long* tl_cyc;  // this workgroup's and item's slots (null past the first 1024 workgroups)
+#endif
 };
 
 __device__ __forceinline__ void dma16(buf_rsrc r, void* dst, uint32_t voff, uint32_t soff) {
@@ -196,6 +206,9 @@ __device__ __forceinline__ void tile_pass(const W4StreamParams& p, const TileLds
 #pragma unroll
   for (int f = 0; f < NF; ++f) bc[f] = dequant8(wf[f].x);
 
+#ifdef DFLASH_TIMELINE
+  const unsigned long long tl_loop = __builtin_amdgcn_s_memtime();
+#endif
   auto step = [&](int kb, auto sa_tag, auto sw_tag) {
     constexpr int sa = decltype(sa_tag)::value, sw = decltype(sw_tag)::value;
     // the activation stage of k-block kb is complete once this wave's loads older than the
@@ -254,6 +267,9 @@ __device__ __forceinline__ void tile_pass(const W4StreamParams& p, const TileLds
   }
   // no load may land in LDS once the stages are reused
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+#ifdef DFLASH_TIMELINE
+  const unsigned long long tl_epi = __builtin_amdgcn_s_memtime();
+#endif
 
   // epilogue: lane holds rows 16 ms + 4 kq + e of its fragments' column lr
   const int4 d = c.d;
@@ -314,13 +330,30 @@ __device__ __forceinline__ void tile_pass(const W4StreamParams& p, const TileLds
       }
     }
   }
+#ifdef DFLASH_TIMELINE
+  const unsigned long long tl_end = __builtin_amdgcn_s_memtime();
+  if (lane == 0 && c.tl_cyc) {
+    unsigned long long* slot = c.tl_cyc + wave * kTlCycleFields;
+    slot[0] = c.t_ctx - c.t_start;
+    slot[1] = c.t_sync - c.t_ctx;
+    slot[2] = tl_loop - c.t_sync;
+    slot[3] = tl_epi - tl_loop;
+    slot[4] = tl_end - tl_epi;
+    slot[5] = 1;
+  }
+#endif
 }
 
-// One work tile: pass P (up to 96 rows of one slot) times column tile nt of 8 x 16 NF columns
+// One work tile: pass d (expert or -1 for the shared expert, segment start, slot rows, first
+// row of the pass; up to 96 rows of one slot) times column tile nt of 8 x 16 NF columns
 // (gate/up: 8 x 8 NF of each half).
 // rhalf: 0 for every row of the pass, 1 for its first ceil(nsub / 2) subtiles, 2 for the rest.
 template <int kMode, typename ScaleT, int NF>
-__device__ __forceinline__ void run_tile(const W4StreamParams& p, const TileLds& lds, int P, int nt, int rhalf) {
+__device__ __forceinline__ void run_tile(const W4StreamParams& p, const TileLds& lds, int4 d, int nt, int rhalf
+#ifdef DFLASH_TIMELINE
+                                         , unsigned long long* tl_cyc
+#endif
+) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = lane_id(), lr = lane & 15, kq = lane >> 4;
@@ -339,8 +372,12 @@ __device__ __forceinline__ void run_tile(const W4StreamParams& p, const TileLds&
   };
 
   TileCtx c;
+#ifdef DFLASH_TIMELINE
+  c.t_start = __builtin_amdgcn_s_memtime();
+  c.tl_cyc = tl_cyc;
+#endif
   c.nt = nt;
-  c.d = ld_const_int4(p.pass_table, P);
+  c.d = d;
   c.shared = c.d.x < 0;
   c.rows = min(kTileM, c.d.z - c.d.w);
   if (rhalf) {
@@ -390,7 +427,14 @@ __device__ __forceinline__ void run_tile(const W4StreamParams& p, const TileLds&
     c.goff = static_cast<uint32_t>(min(wave * 64 + lane, c.rows - 1)) * 4;
   }
 
+#ifdef DFLASH_TIMELINE
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the pass entry is in
+  c.t_ctx = __builtin_amdgcn_s_memtime();
+#endif
   __syncthreads();  // the previous tile's readers are done with every LDS stage
+#ifdef DFLASH_TIMELINE
+  c.t_sync = __builtin_amdgcn_s_memtime();
+#endif
 
   switch ((c.rows + 15) >> 4) {
     case 1: tile_pass<kMode, ScaleT, 1, NF>(p, lds, c); break;
@@ -443,18 +487,27 @@ __global__ __launch_bounds__(512) void w4_tile_kernel(W4StreamParams p) {
     const int i = tile / ntiles;
     const int P = i < sp ? passes - sp + i : i - sp;
     const int nt = tile - i * ntiles;
+    const int4 d = ld_const_int4(p.pass_table, P);
 #ifdef DFLASH_TIMELINE
     unsigned long long* tl = g_timeline_tile +
         (((kMode == kModeGateUp ? 0 : 1) * kTlWorkgroups + blockIdx.x) * kTlTiles + min(tl_n, kTlTiles - 1)) * 3;
     if (threadIdx.x == 0 && blockIdx.x < kTlWorkgroups) tl[0] = __builtin_amdgcn_s_memrealtime();
 #endif
-    if (whole) run_tile<kMode, ScaleT, 4>(p, lds, P, nt, 0);
-    else run_tile<kMode, ScaleT, 2>(p, lds, P, 2 * nt + (q & 1), pieces == 4 ? 1 + (q >> 1) : 0);
+#ifdef DFLASH_TIMELINE
+    unsigned long long* tl_cyc = blockIdx.x < kTlWorkgroups
+        ? g_timeline_tile_cycles + (((kMode == kModeGateUp ? 0 : 1) * kTlWorkgroups + blockIdx.x) * kTlTiles +
+                                    min(tl_n, kTlTiles - 1)) * kWavesTl * kTlCycleFields
+        : nullptr;
+    if (whole) run_tile<kMode, ScaleT, 4>(p, lds, d, nt, 0, tl_cyc);
+    else run_tile<kMode, ScaleT, 2>(p, lds, d, 2 * nt + (q & 1), pieces == 4 ? 1 + (q >> 1) : 0, tl_cyc);
+#else
+    if (whole) run_tile<kMode, ScaleT, 4>(p, lds, d, nt, 0);
+    else run_tile<kMode, ScaleT, 2>(p, lds, d, 2 * nt + (q & 1), pieces == 4 ? 1 + (q >> 1) : 0);
+#endif
 #ifdef DFLASH_TIMELINE
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0 && blockIdx.x < kTlWorkgroups) {
-      const int4 d = ld_const_int4(p.pass_table, P);
       tl[1] = __builtin_amdgcn_s_memrealtime();
       tl[2] = static_cast<unsigned long long>(min(kTileM, d.z - d.w)) | (static_cast<unsigned long long>(P) << 16) |
               (static_cast<unsigned long long>(tl_n + 1) << 40) | (static_cast<unsigned long long>(whole ? 0 : 1) << 56);
@@ -493,10 +546,16 @@ int timeline_tile_read(void* host, size_t bytes) {
   if (bytes != sizeof(g_timeline_tile)) return 1;
   return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_timeline_tile), bytes) == hipSuccess ? 0 : 1;
 }
+int timeline_tile_cycles_read(void* host, size_t bytes) {
+  if (bytes != sizeof(g_timeline_tile_cycles)) return 1;
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_timeline_tile_cycles), bytes) == hipSuccess ? 0 : 1;
+}
 int timeline_tile_clear() {
   void* ptr = nullptr;
   if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_timeline_tile)) != hipSuccess) return 1;
-  return hipMemset(ptr, 0, sizeof(g_timeline_tile)) == hipSuccess ? 0 : 1;
+  if (hipMemset(ptr, 0, sizeof(g_timeline_tile)) != hipSuccess) return 1;
+  if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_timeline_tile_cycles)) != hipSuccess) return 1;
+  return hipMemset(ptr, 0, sizeof(g_timeline_tile_cycles)) == hipSuccess ? 0 : 1;
 }
 #endif
 

@@ -13,8 +13,9 @@ markdown:
   ended (waves w and w + 4 share a SIMD);
 * T=2048 prefill, gate/up and down tile launches: work items per workgroup,
   the spread of workgroup end times, the median whole-tile duration by 16-row
-  subtile count, and the count and median duration of the pieces the last
-  tiles are split into.
+  subtile count, the count and median duration of the pieces the last
+  tiles are split into, and where a wave's time goes inside a work item
+  (set-up, k-loop, epilogue).
 
 The timestamps come from thread 0 (lane 0 of each wave for the k-loop ends)
 after the workgroup's own stores have completed; they include the cost of the
@@ -116,6 +117,8 @@ def tile_report(lib, pkg, device, reps: int) -> list[str]:
     blocks = [torch.randn((2048, 2048), device=device, generator=gen).to(torch.bfloat16) for _ in range(2)]
     ws = torch.empty(pkg.ops.moe_workspace_bytes(2048, 2048, 512, 256, 8, 128, True), dtype=torch.uint8, device=device)
     buf = np.zeros(2 * WORKGROUPS * TILES * 3, dtype=np.uint64)
+    cyc = np.zeros(2 * WORKGROUPS * TILES * 8 * 6, dtype=np.uint64)
+    cyc_sum = np.zeros((2, 6), dtype=np.float64)
     for j in range(3):
         pkg.ops.moe_w4a16(blocks[j % 2], gu, dn, top_k=8, router_weight=router, shared=sh, workspace=ws)
     torch.cuda.synchronize()
@@ -127,6 +130,9 @@ def tile_report(lib, pkg, device, reps: int) -> list[str]:
         torch.cuda.synchronize()
         if lib.dflash_timeline_read(1, buf.ctypes.data, buf.nbytes):
             raise RuntimeError("dflash_timeline_read failed")
+        if lib.dflash_timeline_read(2, cyc.ctypes.data, cyc.nbytes):
+            raise RuntimeError("dflash_timeline_read failed")
+        cyc_sum += cyc.reshape(2, -1, 6).astype(np.float64).sum(axis=1)
         t = buf.reshape(2, WORKGROUPS, TILES, 3).astype(np.int64)
         for m, name in enumerate(("gate/up", "down")):
             used = t[m, :, :, 2] > 0
@@ -145,7 +151,14 @@ def tile_report(lib, pkg, device, reps: int) -> list[str]:
                 s[f"sub{sub}"].append(d)
             s["pieces"].append(int(piece.sum()))
             s["piece_us"].extend((en - st)[piece].tolist())
-    for name, s in stats.items():
+            # a workgroup's consecutive items: the queue claim between them
+            nxt = used[:, 1:] & used[:, :-1]
+            s["gap"].extend((st[:, 1:] - en[:, :-1])[nxt].tolist())
+    for m, name in enumerate(stats):
+        s = stats[name]
+        ids, bar, first, loop, epi, n = cyc_sum[m]
+        pro = ids + bar + first
+        whole = loop + epi + pro
         hist = np.bincount(s["per_wg"])
         pieces = s["pieces"][0]
         out += [f"**{name} launch**: {s['tiles'][0]} work items ({s['tiles'][0] - pieces} whole tiles, {pieces} "
@@ -157,7 +170,16 @@ def tile_report(lib, pkg, device, reps: int) -> list[str]:
                 ", ".join(f"{k[3:]}: {np.median(v) / 100:.1f} ({len(v) // reps} tiles)"
                           for k, v in sorted(s.items()) if k.startswith("sub")),
                 f"- pieces: median {np.median(s['piece_us']) / 100 if s['piece_us'] else 0:.1f} us, "
-                f"max {max(s['piece_us'], default=0) / 100:.1f} us", ""]
+                f"max {max(s['piece_us'], default=0) / 100:.1f} us",
+                f"- a wave's time per work item (s_memtime cycles, summed over waves and items, {int(n)} "
+                f"samples): set-up {pro / whole:.1%} (pass entry {ids / whole:.1%}, barrier with the row "
+                f"id loads and the previous item's stores {bar / whole:.1%}, first stage loads "
+                f"{first / whole:.1%}), "
+                f"k-loop {loop / whole:.1%}, "
+                f"epilogue {epi / whole:.1%}; mean item {whole / max(n, 1):.0f} cycles",
+                f"- between a workgroup's consecutive items (the queue claim): median "
+                f"{np.median(s['gap']) / 100 if s['gap'] else 0:.2f} us, p90 "
+                f"{np.percentile(s['gap'], 90) / 100 if s['gap'] else 0:.2f} us", ""]
     return out
 
 
