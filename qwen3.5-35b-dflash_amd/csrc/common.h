@@ -36,8 +36,10 @@ __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70)
 
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS operations
 // (lgkmcnt(0)) but not for its vector-memory loads still in flight.
-// __syncthreads() also waits for vmcnt(0), i.e. for a prefetch pipeline's worth
-// of outstanding global loads, every time.  The empty asm statements keep the
+// __syncthreads() waits for whatever loads the compiler's counter tracking still
+// sees (often vmcnt(0), a prefetch pipeline's worth of outstanding global loads),
+// but direct-to-LDS loads issued in an earlier iteration of a loop can be
+// invisible to it: it may then be a bare s_barrier.  The empty asm statements keep the
 // compiler from moving memory accesses across the barrier.
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");

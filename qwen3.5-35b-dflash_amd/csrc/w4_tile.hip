@@ -120,6 +120,15 @@ __device__ __forceinline__ void dma_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// Wait until at most kPending of this wave's memory loads are outstanding (no barrier)
+template <int kPending>
+__device__ __forceinline__ void dma_wait() {
+  static_assert(kPending < 16, "vmcnt field");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | kPending);  // vmcnt(kPending)
+  asm volatile("" ::: "memory");
+}
+
 // scheduling-group masks of __builtin_amdgcn_sched_group_barrier
 constexpr int kSchedValu = 0x002, kSchedMfma = 0x008, kSchedDsRead = 0x100;
 
@@ -240,7 +249,14 @@ __device__ __forceinline__ void tile_pass(const W4StreamParams& p, const TileLds
         for (int f = 0; f < NF; ++f) u[ms][f] = mfma16x16x32(a[ms], bc[f], u[ms][f]);
         if (j < 3) a[ms] = lds.a[sa][(ms * 4 + j + 1) * 64 + lane];
       }
-      if (j == 3) read_w(wf, s_next, kb + 1, Idx<(sw + 1) % kWStages>{});
+      if (j == 3) {
+        // the weights and scales of k-block kb + 1 are in once only this step's loads (the
+        // activations of kb + 1 and the weights of kb + 2) may be pending.  The wait is written
+        // out: the compiler's own wait for a direct-to-LDS load is dropped here when a wait
+        // ahead of the loop has already drained the counter
+        dma_wait<NF + 1>();
+        read_w(wf, s_next, kb + 1, Idx<(sw + 1) % kWStages>{});
+      }
 #pragma unroll
       for (int f = 0; f < NF; ++f) bc[f] = dequant8(word(wf[f], (j + 1) & 3));
       // k-step 0 also holds the scale ratios and the rescale (4 NF FMAs per subtile), k-step 3
