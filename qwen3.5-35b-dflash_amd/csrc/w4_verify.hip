@@ -797,12 +797,12 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
         l_w = wbase + row0 * rb;
         l_s = sbase + row0 * ng * static_cast<int64_t>(sizeof(ScaleT));
       };
-      // ring of k-blocks in flight: two 16-byte weight loads and the two group scales of the lane's rows
+      // ring of k-blocks in flight: two 16-byte weight loads and one group scale per lane
       uint4 wbuf[kVDepth][2];
-      uint32_t sbuf[kVDepth][2];
+      uint32_t sbuf[kVDepth][1];
       // Loads are issued unconditionally (past the range they repeat its last k-block, never
       // computed): a load under a branch would make the compiler drain the queue at the loop edge.
-      auto issue = [&](uint4 (&dst)[2], uint32_t (&sdst)[2]) {
+      auto issue = [&](uint4 (&dst)[2], uint32_t (&sdst)[1]) {
         const int lc = max(min(lg, g1 - 1), 0);
         const int ur = lc / kNKB, kb = lc - ur * kNKB;
         if (ur != l_ur) {
@@ -811,9 +811,10 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
         }
         dst[0] = *reinterpret_cast<const uint4*>(l_w + wlane + kb * wkb);
         dst[1] = *reinterpret_cast<const uint4*>(l_w + second * rb + wlane + kb * wkb);
+        // one scale load per lane: lanes 0-31 take tile 0's, lanes 32-63 tile 1's (the lane's
+        // row either way); the compute swaps the halves
         const ScaleT* sp = reinterpret_cast<const ScaleT*>(l_s) + slane + (kb >> gshift) * skb;
-        sdst[0] = load_scale_bits(sp);
-        sdst[1] = load_scale_bits(sp + second * ng);
+        sdst[0] = load_scale_bits(lane >= 32 ? sp + second * ng : sp);
         ++lg;
       };
       // the first k-blocks go out before the activations are staged (they do not depend on them)
@@ -960,8 +961,11 @@ __device__ __forceinline__ void verify_gemm(const VerifyParams& vp, char* lds, c
               acc0 = mfma16x16x32(a[j], dequant8(w0[j]), acc0);
               acc1 = mfma16x16x32(a[j], dequant8(w1[j]), acc1);
             }
-            tot0 += scale_value<ScaleT>(sbuf[i][0]) * acc0;
-            tot1 += scale_value<ScaleT>(sbuf[i][1]) * acc1;
+            // lanes 32 apart share a row: the swap gives every lane tile 0's scale of its row in
+            // the first word and tile 1's in the second
+            const auto sw = __builtin_amdgcn_permlane32_swap(sbuf[i][0], sbuf[i][0], false, false);
+            tot0 += scale_value<ScaleT>(sw[0]) * acc0;
+            tot1 += scale_value<ScaleT>(sw[1]) * acc1;
             // materialise the running sums here: left alone, the compiler sinks the
             // scale-accumulates and keeps every k-block's MFMA result live
             pin(tot0);
