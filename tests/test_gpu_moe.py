@@ -6,6 +6,8 @@ The bf16 output must satisfy max|y - r| / max|r| <= 1e-2 against the
 fp32-accumulated golden (``oracle.moe.moe``: fp32 GEMMs on dequantised
 weights, bf16 SiLU*up intermediate, fp32 combine, one bf16 rounding).
 """
+import contextlib
+
 import numpy as np
 import pytest
 import torch
@@ -270,6 +272,28 @@ def test_moe_repeat_calls_are_identical(pkg, device):
     a = pkg.ops.moe_w4a16(x, gu, dn, top_k=8, router_weight=rw, shared=sh)
     b = pkg.ops.moe_w4a16(x, gu, dn, top_k=8, router_weight=rw, shared=sh)
     assert torch.equal(a, b)
+
+
+@pytest.mark.timeout(300)
+@pytest.mark.parametrize("tokens,pieces,layout", [(2048, 4, "portable"), (2048, 4, "tiled"), (2048, None, "tiled"),
+                                                  (128, None, "tiled")])
+def test_long_block_repeat_calls_are_identical(pkg, device, tokens, pieces, layout):
+    """Bit-identical outputs over repeated calls on the prefill tile kernels (every tail tile in
+    four pieces, or the grid's own split) and on the gathered-pass verify kernels (T=128): a
+    weight stage read before its direct-to-LDS loads have landed shows up as differences from
+    call to call, not as a tolerance failure on every run."""
+    print(f"moe T={tokens} pieces={pieces} {layout}: 4 calls", flush=True)
+    layer = pkg.synthetic.moe_layer(tokens, seed=4)
+    gu, dn, sh = _to(pkg, layer, device)
+    if layout == "tiled":
+        gu, dn, sh = gu.tiled(), dn.tiled(), sh.tiled()
+    x, rw = layer.hidden.to(device), layer.router_weight.to(device)
+    ctx = pkg.ops.tile_pieces(pieces) if pieces else contextlib.nullcontext()
+    with ctx:
+        outs = [pkg.ops.moe_w4a16(x, gu, dn, top_k=8, router_weight=rw, shared=sh) for _ in range(4)]
+    for i, o in enumerate(outs[1:], 1):
+        diff = (o.float() - outs[0].float()).abs()
+        assert torch.equal(o, outs[0]), f"call {i}: {int((diff > 0).sum())} elements differ, max {float(diff.max()):.3g}"
 
 
 @pytest.fixture
