@@ -194,11 +194,12 @@ __device__ __forceinline__ void tile_pass(const W4StreamParams& p, const TileLds
   // the issue order the barrier's load count relies on)
   load_w(0, Idx<0>{});
   load_a(0, Idx<0>{});
+  // down: the rows' routing weights now, for the epilogue (loaded there, each row's weight
+  // would be a dependent memory round trip at the end of every tile); ahead of k-block 1's
+  // weights, so that those stay the newest NF + 1 loads the waits below count on
+  if (kMode == kModeDown && wave * 64 < NSUB * 16) dma4(c.grs, lds.wgt + wave * 64, c.goff, 0);
   asm volatile("" ::: "memory");
   load_w(1, Idx<1>{});
-  // down: the rows' routing weights now, for the epilogue (loaded there, each row's weight
-  // would be a dependent memory round trip at the end of every tile)
-  if (kMode == kModeDown && wave * 64 < NSUB * 16) dma4(c.grs, lds.wgt + wave * 64, c.goff, 0);
 
   f32x4 u[NSUB][NF];  // running sums in units of the current k-block's scale
   float s_prev[NF], s_next[NF];
@@ -211,6 +212,10 @@ __device__ __forceinline__ void tile_pass(const W4StreamParams& p, const TileLds
   for (int ms = 0; ms < NSUB; ++ms)
 #pragma unroll
     for (int f = 0; f < NF; ++f) u[ms][f] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // k-block 0's weights and scales are in once at most the NF + 1 loads of k-block 1's are
+  // pending (this also waits for the activations of k-block 0, which the first k-block's
+  // barrier waits for anyway); written out for the same reason as the k-loop's wait below
+  dma_wait<NF + 1>();
   read_w(wf, s_next, 0, Idx<0>{});
 #pragma unroll
   for (int f = 0; f < NF; ++f) bc[f] = dequant8(wf[f].x);
