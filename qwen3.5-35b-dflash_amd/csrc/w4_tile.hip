@@ -15,9 +15,11 @@
 //     blocks, one per 16-row subtile and 32-k step) and their -136*sum terms,
 //     two stages, one k-block ahead; each wave's own weight fragments (16
 //     columns x 128 k, 16 bytes per lane) and their group scales, three
-//     stages, two k-blocks ahead.  Every stage is its own LDS array, so the
-//     compiler waits only for the loads that filled the array it reads.
-//     One barrier per k-block publishes the activation stage.
+//     stages, two k-blocks ahead.  Every stage is its own LDS array.  One
+//     barrier per k-block publishes the activation stage; a wave reads its
+//     weight stages after counted waits of its own (the compiler's waits for
+//     direct-to-LDS loads are not relied on: it can drop them across loop
+//     iterations).
 //   * the weights are dequantised once per wave to bf16 (136 + q), exact, with
 //     8 VALU operations per 8 weights, and each dequantised word feeds one
 //     v_mfma_f32_16x16x32_bf16 per 16-row subtile;
