@@ -13,8 +13,9 @@
 // timing).
 //
 // Per k-block a lane issues two 16-byte weight loads (16 rows x 64 bytes per
-// tile) and the two group scales of its rows (group size 128 or 256), ahead of
-// the k-block it computes.  Each k-block is
+// tile) and one group scale (group size 128 or 256: its row's in tile 0 for
+// lanes 0-31, in tile 1 for lanes 32-63, swapped across the halves before use),
+// ahead of the k-block it computes.  Each k-block is
 // dequantised in registers (bf16 136+q), multiplied on
 // v_mfma_f32_16x16x32_bf16 against A fragments read from LDS, started from
 // -136*sum(a) and scaled.
