@@ -6,7 +6,7 @@
 // the full reduction length K.  Units form one list (pass-major); each
 // workgroup takes an equal contiguous range of it, and inside the workgroup the
 // range's k-blocks (128 columns of K) are split over the 8 waves in fixed shares
-// (wave_start: 4 parts for each of waves 0-3 to 3 for each of waves 4-7, which
+// (wave_start: 7 parts for each of waves 0-3 to 5 for each of waves 4-7, which
 // share their SIMDs with the older waves).  A unit whose k-blocks fall to several waves
 // is finished by the wave holding its last k-block, after the others left their
 // partial sums in LDS (summed in wave order: the result does not depend on
@@ -62,8 +62,9 @@ constexpr int kVDepthAll = 3;    // k-blocks per wave in flight (loads run 2 ahe
 // Waves w and w + 4 share a SIMD, where the older wave w wins issue arbitration: with equal
 // shares, waves 4-7 finished their k-blocks 16% later (gate/up and down alike), the tail
 // running on half the waves.  Waves 0-3 take kVShareOld parts of the k-blocks to every
-// kVShareYoung of waves 4-7 (4:3 measured best of 1:1, 7:6, 4:3, 11:8: -0.6 us per kernel).
-constexpr int kVShareOld = 4, kVShareYoung = 3;
+// kVShareYoung of waves 4-7 (4:3 measured best of 1:1, 7:6, 4:3, 11:8: -0.6 us per kernel; with
+// one scale load per k-block, 7:5 against 4:3 and 3:2: T=16 layer -0.3 to -0.4 us on two boxes).
+constexpr int kVShareOld = 7, kVShareYoung = 5;
 
 // First k-block of wave w when a workgroup's range of n k-blocks is split by those shares.
 __device__ __forceinline__ int wave_start(int n, int w) {
